@@ -1,0 +1,282 @@
+// fa_common.hpp - device building blocks shared by the gfx950 attention kernels.
+//
+// Matrix-core conventions (CDNA4, wave64).  For a 32x32 MFMA accumulator the
+// element i (0..15) held by lane l sits at
+//     row = 8*(i/4) + 4*(l/32) + (i%4),   col = l%32.
+// An A operand (32 x K) gives lane l row l%32 and E consecutive k-slots of
+// half l/32; a B operand (K x 32) gives lane l column l%32 and the same
+// k-slots.  Because the hardware pairs A and B k-slots identically, any
+// bijection between k-slots and the contracted index may be used as long as
+// A and B agree; the kernels rely on that to feed an accumulator straight
+// back as a B operand (the contracted index then follows the accumulator's
+// row map).
+//
+// 16-bit inputs use v_mfma_f32_32x32x16_{f16,bf16} (KSTEP 16, E 8),
+// fp32 inputs use v_mfma_f32_32x32x2_f32 (KSTEP 2, E 1).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+struct f16_t {};   // tag: IEEE half
+struct bf16_t {};  // tag: bfloat16
+struct f32_t {};   // tag: fp32
+
+// ---------------------------------------------------------------------------
+// Element traits: storage type, conversions, MFMA operand type and instruction.
+// ---------------------------------------------------------------------------
+template <typename Tag> struct Elem;
+
+template <> struct Elem<f16_t> {
+  using S = uint16_t;            // storage
+  using Op = s16x8;              // MFMA operand (8 elements)
+  static constexpr int KSTEP = 16;
+  static constexpr int E = 8;    // k-slots per lane per MFMA
+  static constexpr int CE = 8;   // elements per 16-byte chunk
+  __device__ static inline float to_f(S x) { return (float)__builtin_bit_cast(_Float16, x); }
+  __device__ static inline S from_f(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+  __device__ static inline f32x16 mma(Op a, Op b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h16x8, a),
+                                                  __builtin_bit_cast(h16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <> struct Elem<bf16_t> {
+  using S = uint16_t;
+  using Op = s16x8;
+  static constexpr int KSTEP = 16;
+  static constexpr int E = 8;
+  static constexpr int CE = 8;
+  __device__ static inline float to_f(S x) { return __uint_as_float(((uint32_t)x) << 16); }
+  __device__ static inline S from_f(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+  __device__ static inline f32x16 mma(Op a, Op b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(b16x8, a),
+                                                   __builtin_bit_cast(b16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <> struct Elem<f32_t> {
+  using S = float;
+  using Op = float;
+  static constexpr int KSTEP = 2;
+  static constexpr int E = 1;
+  static constexpr int CE = 4;
+  __device__ static inline float to_f(S x) { return x; }
+  __device__ static inline S from_f(float x) { return x; }
+  __device__ static inline f32x16 mma(Op a, Op b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+};
+
+__device__ inline f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// Row of element i of a 32x32 accumulator for lane half h.
+__device__ constexpr inline int acc_row(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
+
+// ---------------------------------------------------------------------------
+// Operand loads.  E elements at `p` (16 bytes for 16-bit types, 4 for fp32).
+// ---------------------------------------------------------------------------
+template <typename Tag>
+__device__ inline typename Elem<Tag>::Op load_op(const typename Elem<Tag>::S* p) {
+  if constexpr (Elem<Tag>::E == 8) {
+    return *reinterpret_cast<const s16x8*>(p);
+  } else {
+    return *p;
+  }
+}
+
+template <typename Tag>
+__device__ inline typename Elem<Tag>::Op zero_op() {
+  if constexpr (Elem<Tag>::E == 8) {
+    s16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+    return z;
+  } else {
+    return 0.f;
+  }
+}
+
+// Pack accumulator elements [8*j .. 8*j+7] (16-bit) or element j (fp32) of a
+// 32x32 fp32 tile into a B operand whose k-slots follow the tile's row map.
+template <typename Tag>
+__device__ inline typename Elem<Tag>::Op pack_op(const f32x16& acc, int j) {
+  using EL = Elem<Tag>;
+  if constexpr (EL::E == 8) {
+    s16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (short)EL::from_f(acc[8 * j + e]);
+    return r;
+  } else {
+    return acc[j];
+  }
+}
+
+// A operand read from a transposed LDS tile T[row][col] (col contiguous) where
+// the k-slots follow an accumulator row map: slot e of lane half h reads
+// column base + acc_row(8*j + e, h) (16-bit) or base + acc_row(j, h) (fp32).
+template <typename Tag>
+__device__ inline typename Elem<Tag>::Op lds_op_rowmap(const typename Elem<Tag>::S* row, int j, int h) {
+  using EL = Elem<Tag>;
+  if constexpr (EL::E == 8) {
+    // slots 0..3 -> cols 16*(j/2)... see acc_row: for i = 8*(j%2) + e,
+    // acc_row = 16*(j%2) + 8*(e/4) + 4h + (e%4) within the 32-row block j/2.
+    const int base = 32 * (j >> 1) + 16 * (j & 1) + 4 * h;
+    s16x4 lo = *reinterpret_cast<const s16x4*>(row + base);
+    s16x4 hi = *reinterpret_cast<const s16x4*>(row + base + 8);
+    s16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return r;
+  } else {
+    const int blk = j >> 4, i = j & 15;
+    return row[32 * blk + acc_row(i, h)];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane helpers (wave64).
+// ---------------------------------------------------------------------------
+__device__ inline float xor32(float x) { return __shfl_xor(x, 32, 64); }
+
+// ---------------------------------------------------------------------------
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as easy
+// as 1, 2, 3", SC'11).  Counter = 64-bit element offset, key = 64-bit seed.
+// Returns a uniform float in [0, 1) from the first output word.
+// ---------------------------------------------------------------------------
+__device__ inline float philox_uniform(uint64_t seed, uint64_t offset) {
+  uint32_t c0 = (uint32_t)offset, c1 = (uint32_t)(offset >> 32), c2 = 0u, c3 = 0u;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
+  const uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    uint32_t hi0 = __umulhi(M0, c0), lo0 = M0 * c0;
+    uint32_t hi1 = __umulhi(M1, c2), lo1 = M1 * c2;
+    uint32_t n0 = hi1 ^ c1 ^ k0;
+    uint32_t n1 = lo1;
+    uint32_t n2 = hi0 ^ c3 ^ k1;
+    uint32_t n3 = lo0;
+    c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+    k0 += W0; k1 += W1;
+  }
+  return (float)(c0 >> 8) * (1.0f / 16777216.0f);
+}
+
+// ---------------------------------------------------------------------------
+// Score modifiers, applied in the log2 domain in the reference order
+// scale -> softcap -> bias -> ALiBi -> mask (reference _common.py:276-308).
+// ---------------------------------------------------------------------------
+struct Mods {
+  float scale_log2;   // softmax_scale * log2(e)
+  float cap2;         // softcap * log2(e), 0 = off
+  const void* bias;   // already offset to (batch, head); NULL = off
+  int bias_f32;       // bias element type: 1 fp32, 0 q dtype
+  int bias_bf16;      // q dtype is bf16 (only meaningful when !bias_f32)
+  int64_t bias_sm, bias_sn;
+  float alibi_log2;   // slope * log2(e), 0 = off
+  int has_alibi;
+  int causal, wl, wr; // window sides (-1 = unbounded)
+  int off;            // seqlen_k - seqlen_q (bottom-right alignment)
+  int seqlen_k;
+  float drop_p;       // 0 = off
+  float drop_scale;   // 1 / (1 - p)
+  uint64_t drop_seed;
+  uint64_t drop_base; // ((b*Hq + h) * Sq) for the element offset
+  int64_t drop_sk;    // Sk of the dense problem
+};
+
+__device__ inline float tanh_fast(float y) {
+  // tanh(y) = sign(y) * (1 - e^{-2|y|}) / (1 + e^{-2|y|}), e^{-2|y|} <= 1.
+  float a = fabsf(y);
+  float t = __expf(-2.f * a);
+  float r = (1.f - t) / (1.f + t);
+  return copysignf(r, y);
+}
+
+__device__ inline bool keep_pos(const Mods& md, int m, int n) {
+  const int qp = m + md.off;
+  bool k = n < md.seqlen_k;
+  if (md.causal) k = k && (n <= qp);
+  if (md.wl >= 0) k = k && (n >= qp - md.wl);
+  if (md.wr >= 0) k = k && (n <= qp + md.wr);
+  return k;
+}
+
+__device__ inline float load_bias(const Mods& md, int m, int n) {
+  const int64_t o = (int64_t)m * md.bias_sm + (int64_t)n * md.bias_sn;
+  if (md.bias_f32) return reinterpret_cast<const float*>(md.bias)[o];
+  uint16_t b = reinterpret_cast<const uint16_t*>(md.bias)[o];
+  return md.bias_bf16 ? Elem<bf16_t>::to_f(b) : Elem<f16_t>::to_f(b);
+}
+
+// Full modifier chain on one raw dot product s (no mask).  Returns the log2
+// domain score and, through tcap, tanh(.) of the softcap (for the backward).
+template <bool MODS>
+__device__ inline float score(const Mods& md, float s, int m, int n, float& tcap) {
+  float x = s * md.scale_log2;
+  tcap = 0.f;
+  if constexpr (MODS) {
+    if (md.cap2 > 0.f) {
+      tcap = tanh_fast(x / md.cap2);
+      x = md.cap2 * tcap;
+    }
+    if (md.bias) x += load_bias(md, m, n) * kLog2e;
+    if (md.has_alibi) x -= md.alibi_log2 * fabsf((float)(n - m - md.off));
+  }
+  return x;
+}
+
+__device__ inline bool dropout_keep(const Mods& md, int m, int n) {
+  const uint64_t o = (md.drop_base + (uint64_t)m) * (uint64_t)md.drop_sk + (uint64_t)n;
+  return philox_uniform(md.drop_seed, o) > md.drop_p;
+}
+
+// Visibility of a (rows [m0, m0+mr), keys [n0, n0+nr)) rectangle under the
+// position masks: 0 = fully hidden, 1 = partially, 2 = fully visible.
+__device__ inline int rect_visibility(const Mods& md, int m0, int mr, int n0, int nr) {
+  const int n1 = n0 + nr - 1;
+  const int q0 = m0 + md.off, q1 = m0 + mr - 1 + md.off;
+  if (n0 >= md.seqlen_k) return 0;
+  if (md.causal && n0 > q1) return 0;
+  if (md.wl >= 0 && n1 < q0 - md.wl) return 0;
+  if (md.wr >= 0 && n0 > q1 + md.wr) return 0;
+  bool full = n1 < md.seqlen_k;
+  if (md.causal) full = full && (n1 <= q0);
+  if (md.wl >= 0) full = full && (n0 >= q1 - md.wl);
+  if (md.wr >= 0) full = full && (n1 <= q0 + md.wr);
+  return full ? 2 : 1;
+}
+
+// Bounded varlen interval (reference varlen.py:21-27).
+__device__ inline void bounded_seq(const int32_t* cu, int b, int total, int& start, int& len) {
+  int s = cu[b], e = cu[b + 1];
+  s = min(max(s, 0), total);
+  e = min(max(e, 0), total);
+  start = s;
+  len = max(e - s, 0);
+}
+
+// Linear workgroup id remapped so that consecutive logical ids land on the
+// same XCD (the hardware deals workgroups round-robin over 8 XCDs, each with
+// its own L2).  Only applied when the grid is a multiple of 8.
+__device__ inline int xcd_swizzle(int id, int n) {
+  if ((n & 7) != 0) return id;
+  return (id & 7) * (n >> 3) + (id >> 3);
+}
+
+}  // namespace fa

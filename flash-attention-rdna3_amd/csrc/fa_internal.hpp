@@ -1,0 +1,25 @@
+// fa_internal.hpp - host-side launchers behind the C ABI (fa_api.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/fa_mi355x.h"
+
+namespace fa {
+
+// Each launcher validates nothing beyond what it needs to pick a kernel
+// instantiation; fa_api.cpp has already checked the arguments.  They return
+// hipSuccess, hipErrorInvalidValue for an unsupported configuration, or the
+// launch error.
+hipError_t launch_fwd(const fa_fwd_params& p, hipStream_t stream);
+hipError_t launch_bwd(const fa_bwd_params& p, hipStream_t stream);
+hipError_t launch_decode(const fa_decode_params& p, hipStream_t stream);
+hipError_t launch_paged(const fa_paged_params& p, hipStream_t stream);
+hipError_t launch_tiny(const fa_tiny_params& p, hipStream_t stream);
+
+size_t decode_workspace_bytes(int batch, int heads_q, int seqlen_q, int head_dim, int num_splits);
+
+// Raise a kernel's dynamic LDS limit once per process (gfx950: 160 KiB/CU).
+hipError_t allow_lds(const void* kernel, int bytes);
+
+}  // namespace fa

@@ -1,0 +1,191 @@
+"""ctypes binding of the MI355X C ABI (``include/fa_mi355x.h``).
+
+This module is the only place that touches ``libfa_mi355x.so``.  It mirrors
+the header's parameter structs, checks at load time that their sizes match
+what the library was compiled with, and turns a non-zero status into a
+``RuntimeError`` carrying ``fa_last_error_string()``.  There is no fallback:
+if the library is missing the import of any compute path fails loudly.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch
+
+ABI_VERSION = 1
+DTYPE_CODE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+_LIB_NAME = "libfa_mi355x.so"
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
+
+_i64_4 = ctypes.c_int64 * 4
+_i64_3 = ctypes.c_int64 * 3
+_i64_2 = ctypes.c_int64 * 2
+
+
+class FwdParams(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32), ("dtype", ctypes.c_int32),
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("out", ctypes.c_void_p), ("lse", ctypes.c_void_p),
+        ("q_stride", _i64_4), ("k_stride", _i64_4), ("v_stride", _i64_4),
+        ("out_stride", _i64_4), ("lse_stride", _i64_3),
+        ("batch", ctypes.c_int32), ("heads_q", ctypes.c_int32), ("heads_kv", ctypes.c_int32),
+        ("seqlen_q", ctypes.c_int32), ("seqlen_k", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("cu_seqlens_q", ctypes.c_void_p), ("cu_seqlens_k", ctypes.c_void_p),
+        ("total_q", ctypes.c_int32), ("total_k", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+        ("causal", ctypes.c_int32), ("window_left", ctypes.c_int32), ("window_right", ctypes.c_int32),
+        ("softcap", ctypes.c_float),
+        ("bias", ctypes.c_void_p), ("bias_dtype", ctypes.c_int32), ("reserved0", ctypes.c_int32),
+        ("bias_stride", _i64_4),
+        ("alibi_slopes", ctypes.c_void_p),
+        ("dropout_p", ctypes.c_float), ("reserved1", ctypes.c_int32),
+        ("dropout_seed", ctypes.c_uint64),
+    ]
+
+
+class BwdParams(ctypes.Structure):
+    _fields_ = [
+        ("fwd", FwdParams),
+        ("dout", ctypes.c_void_p), ("dq", ctypes.c_void_p), ("dk", ctypes.c_void_p),
+        ("dv", ctypes.c_void_p), ("delta", ctypes.c_void_p),
+        ("dout_stride", _i64_4), ("dq_stride", _i64_4), ("dk_stride", _i64_4),
+        ("dv_stride", _i64_4), ("delta_stride", _i64_3),
+    ]
+
+
+class DecodeParams(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32), ("dtype", ctypes.c_int32),
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("out", ctypes.c_void_p),
+        ("q_stride", _i64_4), ("k_stride", _i64_4), ("v_stride", _i64_4), ("out_stride", _i64_4),
+        ("batch", ctypes.c_int32), ("heads_q", ctypes.c_int32), ("heads_kv", ctypes.c_int32),
+        ("seqlen_q", ctypes.c_int32), ("seqlen_k", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("cache_seqlens", ctypes.c_void_p), ("cache_seqlens_stride", ctypes.c_int64),
+        ("softmax_scale", ctypes.c_float), ("num_splits", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+    ]
+
+
+class PagedParams(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32), ("dtype", ctypes.c_int32),
+        ("q", ctypes.c_void_p), ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+        ("out", ctypes.c_void_p), ("block_table", ctypes.c_void_p), ("context_lens", ctypes.c_void_p),
+        ("q_stride", _i64_3), ("k_stride", _i64_4), ("v_stride", _i64_4), ("out_stride", _i64_3),
+        ("block_table_stride", _i64_2), ("context_lens_stride", ctypes.c_int64),
+        ("batch", ctypes.c_int32), ("heads_q", ctypes.c_int32), ("heads_kv", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("num_blocks", ctypes.c_int32), ("block_size", ctypes.c_int32),
+        ("max_blocks", ctypes.c_int32), ("num_splits", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float), ("reserved0", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+    ]
+
+
+class TinyParams(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32), ("seqlen", ctypes.c_int32),
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("out", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+        ("q_stride", _i64_4), ("k_stride", _i64_4), ("v_stride", _i64_4),
+        ("out_stride", _i64_4), ("bias_stride", _i64_4),
+        ("batch", ctypes.c_int32), ("heads", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float), ("reserved0", ctypes.c_int32),
+    ]
+
+
+_STRUCTS = (FwdParams, BwdParams, DecodeParams, PagedParams, TinyParams)
+EXPORTS = (
+    "fa_abi_version", "fa_last_error_string", "fa_params_size", "fa_decode_workspace_bytes",
+    "fa_fwd", "fa_bwd", "fa_decode_splitk", "fa_decode_paged", "fa_tiny_fwd_f32",
+)
+
+_lib = None
+_lock = threading.Lock()
+
+
+def library_path():
+    return _LIB_PATH
+
+
+def lib():
+    """Load (once) and return the native library; raise if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(
+                f"fa_rdna3 native library not found at {_LIB_PATH}; build it with "
+                "`python -c 'import __graft_entry__; __graft_entry__.build()'` or "
+                "`make -C flash-attention-rdna3_amd/csrc`")
+        handle = ctypes.CDLL(_LIB_PATH)
+        handle.fa_abi_version.restype = ctypes.c_int
+        handle.fa_last_error_string.restype = ctypes.c_char_p
+        handle.fa_params_size.restype = ctypes.c_size_t
+        handle.fa_params_size.argtypes = [ctypes.c_int]
+        handle.fa_decode_workspace_bytes.restype = ctypes.c_size_t
+        handle.fa_decode_workspace_bytes.argtypes = [ctypes.c_int] * 5
+        for name, struct in (("fa_fwd", FwdParams), ("fa_bwd", BwdParams),
+                             ("fa_decode_splitk", DecodeParams), ("fa_decode_paged", PagedParams),
+                             ("fa_tiny_fwd_f32", TinyParams)):
+            fn = getattr(handle, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]
+        if handle.fa_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{_LIB_NAME} ABI {handle.fa_abi_version()} != binding ABI {ABI_VERSION}")
+        for which, struct in enumerate(_STRUCTS):
+            if handle.fa_params_size(which) != ctypes.sizeof(struct):
+                raise RuntimeError(
+                    f"{struct.__name__} layout mismatch: library {handle.fa_params_size(which)} bytes, "
+                    f"binding {ctypes.sizeof(struct)} bytes")
+        _lib = handle
+        return _lib
+
+
+def _check(rc, what):
+    if rc != 0:
+        msg = lib().fa_last_error_string().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {rc}): {msg}")
+
+
+def _stream(tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(tensor.device).cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def call(name, params, device_tensor):
+    """Invoke an fa_* entry point on the current stream of the tensor's device."""
+    fn = getattr(lib(), name)
+    _check(fn(ctypes.byref(params), _stream(device_tensor)), name)
+
+
+def decode_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits):
+    return int(lib().fa_decode_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits))
+
+
+def kernel_ready(t):
+    """Return ``t`` or a contiguous copy so rows satisfy the ABI's vector-load
+    contract (unit last stride, 16-byte aligned row starts)."""
+    esize = t.element_size()
+    ok = t.stride(-1) == 1 or t.shape[-1] == 1
+    ok = ok and t.data_ptr() % 16 == 0
+    ok = ok and all((s * esize) % 16 == 0 for s, n in zip(t.stride()[:-1], t.shape[:-1]) if n > 1)
+    if ok and t.stride(-1) == 1:
+        return t
+    return t.contiguous()
+
+
+def strides(t, n=None):
+    """Element strides of ``t`` for the ABI: size-1 dims (never stepped over)
+    get stride 0, and the last dim is contiguous (see ``kernel_ready``)."""
+    st = [s if sz > 1 else 0 for s, sz in zip(t.stride(), t.shape)]
+    st[-1] = 1
+    return st if n is None else st[:n]

@@ -1,0 +1,245 @@
+/*
+ * fa_mi355x.h - C ABI of the MI355X (gfx950) FlashAttention-2 kernels.
+ *
+ * Every entry point replaces one group of Triton launch sites of the reference
+ * (chelokot/flash-attention-rdna3, fa_rdna3/interface.py).  The boundary is
+ * plain C: device pointers, element strides, sizes, scalars and an opaque
+ * stream handle (a hipStream_t, or NULL for the null stream).  No torch types
+ * cross it.
+ *
+ * Conventions
+ *   - All strides are in ELEMENTS of the tensor they describe (not bytes), so
+ *     arbitrary views (transposes, packed qkv, strided metadata) are accepted.
+ *   - The caller owns every buffer, including LSE, delta and the decode split
+ *     workspace; the library never allocates device memory and keeps no
+ *     pointer after a call returns.
+ *   - Calls are asynchronous on `stream` and never synchronise the host.
+ *   - Every call returns FA_OK (0) or an fa_status code; a human-readable
+ *     message for the last failure on the calling thread is available from
+ *     fa_last_error_string().  Nothing throws across the ABI.
+ *   - Argument contracts are checked by the host layer above (same messages as
+ *     the reference's fa_rdna3/_validation.py); this layer re-checks only what
+ *     would make a kernel read or write out of bounds (shape limits, dtype
+ *     codes, head dims) and rejects it with FA_ERR_INVALID / FA_ERR_UNSUPPORTED.
+ */
+#ifndef FA_MI355X_H
+#define FA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+typedef enum fa_dtype {
+  FA_DTYPE_F16 = 0,
+  FA_DTYPE_BF16 = 1,
+  FA_DTYPE_F32 = 2
+} fa_dtype;
+
+typedef enum fa_status {
+  FA_OK = 0,
+  FA_ERR_INVALID = 1,     /* malformed arguments (null pointer, bad size) */
+  FA_ERR_UNSUPPORTED = 2, /* valid but not implemented (head dim, dtype) */
+  FA_ERR_LAUNCH = 3       /* hipGetLastError() reported a launch failure */
+} fa_status;
+
+/*
+ * Forward attention with natural-log LSE, dense or packed-varlen.
+ *
+ * Replaces the `_attention_forward[grid](...)` launch of `_forward`
+ * (interface.py:154-199, launch at :180) and the
+ * `_attention_forward_varlen[grid](...)` launch of `_forward_varlen`
+ * (interface.py:482-511, launch at :494).
+ *
+ * Dense:  q (B,Hq,Sq,D), k/v (B,Hkv,Sk,D), out like q, lse (B,Hq,Sq) fp32.
+ * Varlen: cu_seqlens_q != NULL.  q (Tq,Hq,D) is described with
+ *         q_stride = {0, stride(1), stride(0), stride(2)} (batch, head, row,
+ *         dim); lse (Hq,Tq) with lse_stride = {0, stride(0), stride(1)}.
+ *         Sequence b covers rows [cu_q[b], cu_q[b+1]) clamped to [0, total_q]
+ *         (reference varlen.py:21-27); seqlen_q/seqlen_k carry max_seqlen.
+ */
+typedef struct fa_fwd_params {
+  int32_t abi_version; /* must be FA_ABI_VERSION */
+  int32_t dtype;       /* fa_dtype of q, k, v, out */
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  float* lse;
+  int64_t q_stride[4];   /* batch, head, row, dim */
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t out_stride[4];
+  int64_t lse_stride[3]; /* batch, head, row */
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;
+  int32_t seqlen_q; /* dense: Sq.  varlen: max_seqlen_q */
+  int32_t seqlen_k; /* dense: Sk.  varlen: max_seqlen_k */
+  int32_t head_dim; /* 32, 64, 128, 256 or 512 */
+  const int32_t* cu_seqlens_q; /* NULL for dense */
+  const int32_t* cu_seqlens_k;
+  int32_t total_q;
+  int32_t total_k;
+  float softmax_scale;
+  int32_t causal;       /* bottom-right aligned when Sq != Sk */
+  int32_t window_left;  /* -1: unbounded */
+  int32_t window_right; /* -1: unbounded */
+  float softcap;        /* 0: off; else softcap*tanh(s/softcap) */
+  const void* bias;     /* NULL or additive logit bias (B,Hq,Sq,Sk) view */
+  int32_t bias_dtype;   /* fa_dtype of bias (q dtype or FA_DTYPE_F32) */
+  int32_t reserved0;
+  int64_t bias_stride[4]; /* broadcast dims carry stride 0 */
+  const float* alibi_slopes; /* NULL or (Hq,) fp32 */
+  float dropout_p;
+  int32_t reserved1;
+  uint64_t dropout_seed;
+} fa_fwd_params;
+
+/*
+ * Backward: delta precompute, dK/dV and dQ in one call (three kernels on the
+ * same stream, no atomics, deterministic).
+ *
+ * Replaces `_backward` (interface.py:202-277, launches at :226, :236, :258)
+ * and `_backward_varlen` (interface.py:514-580, launches at :531, :541, :562).
+ * `delta` is caller-provided scratch shaped like lse.  Gradients are written
+ * in the dtype of q/k/v with their own strides.
+ */
+typedef struct fa_bwd_params {
+  fa_fwd_params fwd; /* q, k, v, out, lse and every option of the forward */
+  const void* dout;
+  void* dq;
+  void* dk;
+  void* dv;
+  float* delta;
+  int64_t dout_stride[4];
+  int64_t dq_stride[4];
+  int64_t dk_stride[4];
+  int64_t dv_stride[4];
+  int64_t delta_stride[3];
+} fa_bwd_params;
+
+/*
+ * Split-K decode with an LSE-weighted merge.
+ *
+ * Replaces `flash_attention_decode`'s two launches (interface.py:427-479,
+ * `_attention_split` at :458 and `_attention_combine` at :471).
+ * q (B,Hq,Sq,D), k/v (B,Hkv,Sk,D), out like q.  Non-causal.  When
+ * cache_seqlens != NULL, sequence b only attends keys [0, cache_seqlens[b])
+ * (clamped to [0, Sk]); a length of 0 yields a zero output row.
+ * `workspace` must hold fa_decode_workspace_bytes(...) bytes.
+ */
+typedef struct fa_decode_params {
+  int32_t abi_version;
+  int32_t dtype; /* FA_DTYPE_F16 or FA_DTYPE_BF16 */
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int64_t q_stride[4];
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t out_stride[4];
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;
+  int32_t seqlen_q;
+  int32_t seqlen_k;
+  int32_t head_dim;
+  const int32_t* cache_seqlens; /* NULL: every sequence has Sk keys */
+  int64_t cache_seqlens_stride;
+  float softmax_scale;
+  int32_t num_splits; /* 1..64 */
+  void* workspace;
+} fa_decode_params;
+
+/*
+ * Paged-KV decode walking a block table (vLLM-style cache).
+ *
+ * Replaces `flash_attention_decode_paged`'s launches (interface.py:643-728,
+ * `_attention_decode_paged` at :704 and `_attention_combine` at :720).
+ * q (B,Hq,D); k_cache/v_cache (num_blocks, block_size, Hkv, D);
+ * block_table (B, max_blocks) int32; context_lens (B,) int32.  Context is
+ * clamped to [0, max_blocks*block_size] and physical ids outside
+ * [0, num_blocks) contribute nothing (reference paged.py:37-38, :58-59).
+ */
+typedef struct fa_paged_params {
+  int32_t abi_version;
+  int32_t dtype; /* FA_DTYPE_F16 or FA_DTYPE_BF16 */
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  void* out;
+  const int32_t* block_table;
+  const int32_t* context_lens;
+  int64_t q_stride[3];  /* batch, head, dim */
+  int64_t k_stride[4];  /* block, position, head, dim */
+  int64_t v_stride[4];
+  int64_t out_stride[3];
+  int64_t block_table_stride[2];
+  int64_t context_lens_stride;
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;
+  int32_t head_dim;
+  int32_t num_blocks;
+  int32_t block_size; /* power of two, 1..256 */
+  int32_t max_blocks; /* columns of block_table */
+  int32_t num_splits; /* 1..64 */
+  float softmax_scale;
+  int32_t reserved0;
+  void* workspace; /* fa_decode_workspace_bytes(batch, heads_q, 1, head_dim, num_splits) */
+} fa_paged_params;
+
+/*
+ * Short-sequence fp32 inference forward (D = 128, S <= 32, non-causal).
+ * Replaces the `_attention_tiny_forward` launch (interface.py:84-104).
+ */
+typedef struct fa_tiny_params {
+  int32_t abi_version;
+  int32_t seqlen; /* 1..32, Sq == Sk */
+  const float* q;
+  const float* k;
+  const float* v;
+  float* out;
+  const float* bias; /* NULL or fp32 (B,H,S,S) view */
+  int64_t q_stride[4];
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t out_stride[4];
+  int64_t bias_stride[4];
+  int32_t batch;
+  int32_t heads;
+  float softmax_scale;
+  int32_t reserved0;
+} fa_tiny_params;
+
+/* Version of this header the library was built from (FA_ABI_VERSION). */
+int fa_abi_version(void);
+
+/* Message describing the last non-FA_OK return on the calling thread. */
+const char* fa_last_error_string(void);
+
+/* sizeof() of each params struct as compiled into the library, so a binding
+ * can verify its own layout: which = 0 fwd, 1 bwd, 2 decode, 3 paged, 4 tiny. */
+size_t fa_params_size(int which);
+
+/* Bytes of scratch the split-K and paged decode need for `num_splits`. */
+size_t fa_decode_workspace_bytes(int batch, int heads_q, int seqlen_q,
+                                 int head_dim, int num_splits);
+
+int fa_fwd(const fa_fwd_params* params, void* stream);
+int fa_bwd(const fa_bwd_params* params, void* stream);
+int fa_decode_splitk(const fa_decode_params* params, void* stream);
+int fa_decode_paged(const fa_paged_params* params, void* stream);
+int fa_tiny_fwd_f32(const fa_tiny_params* params, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_MI355X_H */
