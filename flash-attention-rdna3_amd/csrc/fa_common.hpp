@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/fa_mi355x.h"
+
 namespace fa {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -269,6 +271,37 @@ __device__ inline void bounded_seq(const int32_t* cu, int b, int total, int& sta
   e = min(max(e, 0), total);
   start = s;
   len = max(e - s, 0);
+}
+
+// Modifier state of (batch b, query head hq) for a problem whose sequence
+// lengths (after varlen bounding) are sq x sk.
+__device__ inline Mods make_mods(const fa_fwd_params& p, int b, int hq, int sq, int sk) {
+  Mods md;
+  md.scale_log2 = p.softmax_scale * kLog2e;
+  md.cap2 = p.softcap * kLog2e;
+  md.bias = nullptr;
+  md.bias_f32 = p.bias_dtype == FA_DTYPE_F32;
+  md.bias_bf16 = p.dtype == FA_DTYPE_BF16;
+  md.bias_sm = p.bias_stride[2];
+  md.bias_sn = p.bias_stride[3];
+  if (p.bias) {
+    const int64_t o = b * p.bias_stride[0] + hq * p.bias_stride[1];
+    md.bias = md.bias_f32 ? (const void*)(reinterpret_cast<const float*>(p.bias) + o)
+                          : (const void*)(reinterpret_cast<const uint16_t*>(p.bias) + o);
+  }
+  md.has_alibi = p.alibi_slopes != nullptr;
+  md.alibi_log2 = md.has_alibi ? p.alibi_slopes[hq] * kLog2e : 0.f;
+  md.causal = p.causal;
+  md.wl = p.window_left;
+  md.wr = p.window_right;
+  md.off = sk - sq;
+  md.seqlen_k = sk;
+  md.drop_p = p.dropout_p;
+  md.drop_scale = p.dropout_p > 0.f ? 1.f / (1.f - p.dropout_p) : 1.f;
+  md.drop_seed = p.dropout_seed;
+  md.drop_base = ((uint64_t)b * p.heads_q + hq) * (uint64_t)p.seqlen_q;
+  md.drop_sk = p.seqlen_k;
+  return md;
 }
 
 // Linear workgroup id remapped so that consecutive logical ids land on the

@@ -89,31 +89,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(fa_fwd_params p, int num_m_blo
   float* lb = p.lse + b * p.lse_stride[0] + hq * p.lse_stride[1] + (int64_t)q_start * p.lse_stride[2];
   const int64_t qs = p.q_stride[2], ks = p.k_stride[2], vs = p.v_stride[2];
 
-  Mods md;
-  md.scale_log2 = p.softmax_scale * kLog2e;
-  md.cap2 = p.softcap * kLog2e;
-  md.bias = nullptr;
-  md.bias_f32 = p.bias_dtype == FA_DTYPE_F32;
-  md.bias_bf16 = p.dtype == FA_DTYPE_BF16;
-  md.bias_sm = p.bias_stride[2];
-  md.bias_sn = p.bias_stride[3];
-  if (p.bias) {
-    const int64_t o = b * p.bias_stride[0] + hq * p.bias_stride[1];
-    md.bias = md.bias_f32 ? (const void*)(reinterpret_cast<const float*>(p.bias) + o)
-                          : (const void*)(reinterpret_cast<const uint16_t*>(p.bias) + o);
-  }
-  md.has_alibi = p.alibi_slopes != nullptr;
-  md.alibi_log2 = md.has_alibi ? p.alibi_slopes[hq] * kLog2e : 0.f;
-  md.causal = p.causal;
-  md.wl = p.window_left;
-  md.wr = p.window_right;
-  md.off = sk - sq;
-  md.seqlen_k = sk;
-  md.drop_p = p.dropout_p;
-  md.drop_scale = p.dropout_p > 0.f ? 1.f / (1.f - p.dropout_p) : 1.f;
-  md.drop_seed = p.dropout_seed;
-  md.drop_base = ((uint64_t)b * p.heads_q + hq) * (uint64_t)p.seqlen_q;
-  md.drop_sk = p.seqlen_k;
+  const Mods md = make_mods(p, b, hq, sq, sk);
 
   // Key range of the workgroup (reference forward.py:92-127, tightened to the
   // rows that exist).

@@ -1,6 +1,5 @@
 #include "fa_internal.hpp"
 namespace fa {
-hipError_t launch_bwd(const fa_bwd_params&, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_decode(const fa_decode_params&, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_paged(const fa_paged_params&, hipStream_t) { return hipErrorInvalidValue; }
 hipError_t launch_tiny(const fa_tiny_params&, hipStream_t) { return hipErrorInvalidValue; }
