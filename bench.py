@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X FlashAttention path (one JSON line on stdout).
+
+Metric: causal fwd+bwd TFLOP/s at 2x16x2048x128 fp16
+(config 2), with the decode KV-read GB/s of configs 3 (split-K GQA decode)
+and 4 (paged decode) reported beside it.  A "step" is one forward + backward
+of config 2 on synthetic N(0,1) inputs already resident in HBM.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+
+FLOP convention (reference bench/benchmark.py:32-36, :123): forward
+4*B*H*S^2*D / 2 under causal masking, backward 2.5x forward.  Decode bytes
+count every K/V byte of the visible keys once per KV head (+ q and out).
+
+The JSON line carries `roofline` for the dominant kernel (the dK/dV backward
+kernel, timed alone with HIP events on the launch stream) and `cpu_baseline`
+(the CPU oracle (numpy float64) on a bounded sample of the same workload).
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "flash-attention-rdna3_amd"))
+
+import torch  # noqa: E402
+
+# MI355X published peaks.
+PEAK_FP16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+CFG2 = dict(batch=2, heads=16, seqlen=2048, head_dim=128, causal=True, dtype=torch.float16)
+
+
+# ---------------------------------------------------------------------------
+# Seeded workloads of BASELINE.json (inputs drawn on the CPU with
+# torch.Generator().manual_seed(0), cast, then moved to the device).
+# ---------------------------------------------------------------------------
+
+def _gen(seed=0):
+    return torch.Generator().manual_seed(seed)
+
+
+def workload_cfg1(device="cpu"):
+    g = _gen()
+    q, k, v = (torch.randn(1, 16, 1024, 64, generator=g).half().float().to(device) for _ in range(3))
+    return q, k, v, 1.0 / 8.0
+
+
+def workload_cfg2(device="cuda", dtype=torch.float16):
+    g = _gen()
+    shape = (CFG2["batch"], CFG2["heads"], CFG2["seqlen"], CFG2["head_dim"])
+    q, k, v, do = (torch.randn(shape, generator=g).to(dtype).to(device) for _ in range(4))
+    return q, k, v, do, 1.0 / math.sqrt(128)
+
+
+def workload_cfg3(device="cuda"):
+    g = _gen()
+    q = torch.randn(4, 32, 1, 128, generator=g).half()
+    k = torch.randn(4, 8, 8192, 128, generator=g).half()
+    v = torch.randn(4, 8, 8192, 128, generator=g).half()
+    lens = torch.randint(1024, 8193, (4,), generator=_gen()).to(torch.int32)
+    return q.to(device), k.to(device), v.to(device), lens.to(device)
+
+
+def workload_cfg4(device="cuda"):
+    g = _gen()
+    q = torch.randn(4, 32, 128, generator=g).half()
+    kc = torch.randn(4096, 16, 8, 128, generator=g).half()
+    vc = torch.randn(4096, 16, 8, 128, generator=g).half()
+    bt = torch.randperm(4096, generator=_gen()).to(torch.int32).reshape(4, 1024)
+    ctx = torch.full((4,), 16384, dtype=torch.int32)
+    return q.to(device), kc.to(device), vc.to(device), bt.to(device), ctx.to(device)
+
+
+def workload_cfg5(device="cuda"):
+    lengths = torch.randint(128, 2049, (16,), generator=_gen()).tolist()
+    total = sum(lengths)
+    g = _gen()
+    q = torch.randn(total, 32, 128, generator=g).bfloat16()
+    k = torch.randn(total, 8, 128, generator=g).bfloat16()
+    v = torch.randn(total, 8, 128, generator=g).bfloat16()
+    do = torch.randn(total, 32, 128, generator=g).bfloat16()
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32)
+    return lengths, q.to(device), k.to(device), v.to(device), do.to(device), cu.to(device)
+
+
+def cfg2_flops():
+    c = CFG2
+    fwd = 4.0 * c["batch"] * c["heads"] * c["seqlen"] ** 2 * c["head_dim"] / 2
+    return fwd, 2.5 * fwd
+
+
+def cfg3_bytes(lens):
+    return sum(int(n) for n in lens) * 8 * 128 * 2 * 2 + 2 * 4 * 32 * 128 * 2
+
+
+def cfg4_bytes():
+    return 4 * 16384 * 8 * 128 * 2 * 2 + 4 * 1024 * 4 + 2 * 4 * 32 * 128 * 2
+
+
+def cfg5_flops(lengths, window_left=1024):
+    pairs = sum(min(i + 1, window_left + 1) for n in lengths for i in range(n))
+    fwd = 4.0 * 32 * 128 * pairs
+    return fwd, 2.5 * fwd
+
+
+# ---------------------------------------------------------------------------
+# GPU timing helpers
+# ---------------------------------------------------------------------------
+
+def _event_time(fn, iters, stream):
+    """Average ms per call of fn() measured with HIP events on `stream`."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def _flush_buffer(device):
+    return torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=device)
+
+
+def run_cfg2(steps, warmup):
+    from fa_rdna3 import flash_attention
+
+    q, k, v, do, scale = workload_cfg2()
+    q.requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+
+    def step():
+        out = flash_attention(q, k, v, causal=True, softmax_scale=scale)
+        out.backward(do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return dt, (q, k, v, do, scale)
+
+
+def dkdv_roofline(tensors, iters=50):
+    """Time the dK/dV kernel alone (fa_bwd phase 1) with HIP events."""
+    from fa_rdna3 import interface as I
+
+    q, k, v, do, scale = tensors
+    with torch.no_grad():
+        out, lse = I._forward(q.detach(), k.detach(), v.detach(), True, scale, (-1, -1), 0.0, None, None, 0.0, 0)
+        launch = I._backward_launcher(do, q.detach(), k.detach(), v.detach(), out, lse, True, scale,
+                                      (-1, -1), 0.0, None, None, 0.0, 0)
+        launch(0)  # delta, needed by the dK/dV phase
+        for _ in range(5):
+            launch(1)
+        stream = torch.cuda.current_stream()
+        ms = _event_time(lambda: launch(1), iters, stream)
+    fwd, _ = cfg2_flops()
+    flops = 2.0 * fwd  # S recompute, dP, dV, dK: 4 of the 5 algorithmic backward GEMMs
+    achieved = flops / (ms * 1e-3) / 1e12
+    return {"kernel": "bwd_dkdv_kernel<f16,128>", "bound": "mfma", "achieved": round(achieved, 2),
+            "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+            "traffic": None, "avg_us": round(ms * 1e3, 2), "flops_per_launch": flops}
+
+
+def run_decode_configs(iters=50):
+    from fa_rdna3 import flash_attention_decode, flash_attention_decode_paged
+
+    res = {}
+    stream = torch.cuda.current_stream()
+    flush = _flush_buffer("cuda")
+    with torch.no_grad():
+        q, k, v, lens = workload_cfg3()
+        f3 = lambda: flash_attention_decode(q, k, v, cache_seqlens=lens)
+        for _ in range(5):
+            f3()
+        tot = 0.0
+        for _ in range(iters):
+            flush.zero_()
+            tot += _event_time(f3, 1, stream)
+        ms = tot / iters
+        gb = cfg3_bytes(lens.tolist()) / (ms * 1e-3) / 1e9
+        res["cfg3_splitk_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
+                                     "frac_hbm": round(gb / PEAK_HBM_GBS, 4), "l2_flushed": True}
+        del q, k, v
+        q, kc, vc, bt, ctx = workload_cfg4()
+        f4 = lambda: flash_attention_decode_paged(q, kc, vc, bt, ctx, max_context_len=16384)
+        for _ in range(5):
+            f4()
+        tot = 0.0
+        for _ in range(iters):
+            flush.zero_()
+            tot += _event_time(f4, 1, stream)
+        ms = tot / iters
+        gb = cfg4_bytes() / (ms * 1e-3) / 1e9
+        res["cfg4_paged_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
+                                    "frac_hbm": round(gb / PEAK_HBM_GBS, 4), "l2_flushed": True}
+    return res
+
+
+def run_cfg5(iters=5):
+    from fa_rdna3 import flash_attention_varlen
+
+    lengths, q, k, v, do, cu = workload_cfg5()
+    q.requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+    mx = max(lengths)
+
+    def step():
+        out = flash_attention_varlen(q, k, v, cu, cu, mx, mx, causal=True, window_size=(1024, -1), softcap=50.0)
+        out.backward(do)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / iters
+    fwd, bwd = cfg5_flops(lengths)
+    return {"ms": round(dt * 1e3, 3), "TFLOP/s": round((fwd + bwd) / dt / 1e12, 1)}
+
+
+def cpu_baseline(budget_s=20.0):
+    """The CPU oracle (numpy float32 matmuls, all host threads) timed on a
+    bounded sample of config 2: forward + analytic backward of as many
+    (batch, head) slices as fit in the budget, scaled to TFLOP/s."""
+    sys.path.insert(0, ROOT)
+    import numpy as np
+    from oracle import attention as oracle
+
+    g = np.random.default_rng(0)
+    S, D = CFG2["seqlen"], CFG2["head_dim"]
+    q, k, v, do = (g.standard_normal((1, 1, S, D)).astype(np.float32) for _ in range(4))
+    fwd_one = 4.0 * S * S * D / 2
+    done, t0 = 0, time.perf_counter()
+    while True:
+        oracle.attention_forward(q, k, v, causal=True, scale=1 / math.sqrt(D))
+        oracle.attention_backward(q, k, v, do, causal=True, scale=1 / math.sqrt(D))
+        done += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or done >= 32:
+            break
+    tflops = done * 3.5 * fwd_one / el / 1e12
+    return {"value": round(tflops, 5), "unit": "TFLOP/s", "cores": os.cpu_count(), "kind": "port",
+            "sample": f"{done} of 32 (batch, head) slices of config 2 (1x1x2048x128 causal fwd+bwd each), "
+                      f"numpy float64 oracle, {el:.1f}s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip decode/varlen side measurements")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: the attention path is single-GPU in this build "
+              "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    dt, tensors = run_cfg2(args.steps, args.warmup)
+    fwd, bwd = cfg2_flops()
+    value = (fwd + bwd) / dt / 1e12
+    line = {
+        "metric": "fwd+bwd TFLOP/s (2x16x2048x128 causal fp16); decode KV-read GB/s",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic N(0,1), seed 0",
+        "config": {"workload": "cfg2: causal fwd+bwd B=2 H=16 S=2048 D=128 fp16, bottom-right causal",
+                   "global_batch": 2, "seq_len": 2048, "parallelism": "none (1 GPU)"},
+        "frac_of_peak": round(value / PEAK_FP16_TFLOPS, 4),
+    }
+    line["roofline"] = dkdv_roofline(tensors)
+    if not args.no_extras:
+        line["decode"] = run_decode_configs()
+        line["cfg5_varlen"] = run_cfg5()
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

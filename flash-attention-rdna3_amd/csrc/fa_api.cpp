@@ -122,7 +122,7 @@ int fa_fwd(const fa_fwd_params* params, void* stream) {
   return from_hip(fa::launch_fwd(*params, (hipStream_t)stream), "fa_fwd");
 }
 
-int fa_bwd(const fa_bwd_params* params, void* stream) {
+static int bwd_common(const fa_bwd_params* params, int phases, void* stream) {
   if (!params) return fail(FA_ERR_INVALID, "fa_bwd: params is NULL");
   int rc = check_fwd(params->fwd, "fa_bwd");
   if (rc) return rc;
@@ -132,7 +132,14 @@ int fa_bwd(const fa_bwd_params* params, void* stream) {
       !rows_ok(p.dk, p.dk_stride, 4, es) || !rows_ok(p.dv, p.dv_stride, 4, es))
     return fail(FA_ERR_INVALID, "fa_bwd: dout/dq/dk/dv need a unit last stride and 16-byte aligned rows");
   if (!p.delta) return fail(FA_ERR_INVALID, "fa_bwd: delta is NULL");
-  return from_hip(fa::launch_bwd(p, (hipStream_t)stream), "fa_bwd");
+  return from_hip(fa::launch_bwd(p, phases, (hipStream_t)stream), "fa_bwd");
+}
+
+int fa_bwd(const fa_bwd_params* params, void* stream) { return bwd_common(params, 7, stream); }
+
+int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream) {
+  if (phase < 0 || phase > 2) return fail(FA_ERR_INVALID, "fa_bwd_phase: phase %d not in 0..2", phase);
+  return bwd_common(params, 1 << phase, stream);
 }
 
 int fa_decode_splitk(const fa_decode_params* params, void* stream) {

@@ -546,15 +546,15 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(fa_bwd_params p, int num_m_
 
 // ---------------------------------------------------------------------------
 template <typename Tag, int D, bool MODS>
-static hipError_t run_bwd(const fa_bwd_params& p, hipStream_t stream) {
+static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream) {
   const fa_fwd_params& f = p.fwd;
-  {
+  if (phases & 1) {
     dim3 grid((f.seqlen_q + 15) / 16, f.batch * f.heads_q);
     hipLaunchKernelGGL((bwd_delta_kernel<Tag, D>), grid, dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  {
+  if (phases & 2) {
     using C = DkdvCfg<Tag, D>;
     auto kern = bwd_dkdv_kernel<Tag, D, MODS>;
     hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
@@ -565,7 +565,7 @@ static hipError_t run_bwd(const fa_bwd_params& p, hipStream_t stream) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  {
+  if (phases & 4) {
     using C = DqCfg<Tag, D>;
     auto kern = bwd_dq_kernel<Tag, D, MODS>;
     hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
@@ -580,29 +580,29 @@ static hipError_t run_bwd(const fa_bwd_params& p, hipStream_t stream) {
 }
 
 template <typename Tag, bool MODS>
-static hipError_t bwd_by_dim(const fa_bwd_params& p, hipStream_t s) {
+static hipError_t bwd_by_dim(const fa_bwd_params& p, int ph, hipStream_t s) {
   switch (p.fwd.head_dim) {
-    case 32: return run_bwd<Tag, 32, MODS>(p, s);
-    case 64: return run_bwd<Tag, 64, MODS>(p, s);
-    case 128: return run_bwd<Tag, 128, MODS>(p, s);
-    case 256: return run_bwd<Tag, 256, MODS>(p, s);
-    case 512: return run_bwd<Tag, 512, MODS>(p, s);
+    case 32: return run_bwd<Tag, 32, MODS>(p, ph, s);
+    case 64: return run_bwd<Tag, 64, MODS>(p, ph, s);
+    case 128: return run_bwd<Tag, 128, MODS>(p, ph, s);
+    case 256: return run_bwd<Tag, 256, MODS>(p, ph, s);
+    case 512: return run_bwd<Tag, 512, MODS>(p, ph, s);
   }
   return hipErrorInvalidValue;
 }
 
 template <typename Tag>
-static hipError_t bwd_by_mods(const fa_bwd_params& p, hipStream_t s) {
+static hipError_t bwd_by_mods(const fa_bwd_params& p, int ph, hipStream_t s) {
   const fa_fwd_params& f = p.fwd;
   const bool mods = f.softcap > 0.f || f.bias || f.alibi_slopes || f.dropout_p > 0.f;
-  return mods ? bwd_by_dim<Tag, true>(p, s) : bwd_by_dim<Tag, false>(p, s);
+  return mods ? bwd_by_dim<Tag, true>(p, ph, s) : bwd_by_dim<Tag, false>(p, ph, s);
 }
 
-hipError_t launch_bwd(const fa_bwd_params& p, hipStream_t s) {
+hipError_t launch_bwd(const fa_bwd_params& p, int ph, hipStream_t s) {
   switch (p.fwd.dtype) {
-    case FA_DTYPE_F16: return bwd_by_mods<f16_t>(p, s);
-    case FA_DTYPE_BF16: return bwd_by_mods<bf16_t>(p, s);
-    case FA_DTYPE_F32: return bwd_by_mods<f32_t>(p, s);
+    case FA_DTYPE_F16: return bwd_by_mods<f16_t>(p, ph, s);
+    case FA_DTYPE_BF16: return bwd_by_mods<bf16_t>(p, ph, s);
+    case FA_DTYPE_F32: return bwd_by_mods<f32_t>(p, ph, s);
   }
   return hipErrorInvalidValue;
 }

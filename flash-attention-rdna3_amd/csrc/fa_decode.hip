@@ -1,0 +1,402 @@
+// fa_decode.hip - split-K decode and paged-KV decode for gfx950.
+//
+// Same results as the reference's `_attention_split` + `_attention_combine`
+// (fa_rdna3/kernels/decode.py:9-125) and `_attention_decode_paged`
+// (fa_rdna3/kernels/paged.py:16-89): every (sequence, query row) gets
+// softmax(q K^T * scale) V over its visible keys, computed per key split as a
+// normalised partial O plus a natural-log LSE, then merged with weights
+// exp(lse_s - max_s lse) (empty splits, lse = -inf, weigh nothing; an all-empty
+// row is zero).  Paged lookups clamp the context to the block-table capacity
+// and treat physical ids outside [0, num_blocks) as absent keys
+// (reference paged.py:37-38, :58-59).
+//
+// MI355X layout.  Decode is HBM-bound, so the kernel is organised around
+// reading each K/V byte once:
+//  * a workgroup owns one (batch, KV head, split) and packs the whole GQA
+//    group (group heads x Sq query rows) onto the 32 lanes of the MFMA
+//    column axis, so K/V of a KV head are never re-read per query head (the
+//    reference re-reads them Hq/Hkv times);
+//  * its 4 waves walk interleaved 32-key chunks, each through a wave-private
+//    LDS slot (K row-major, V transposed) with the next chunk's 16-byte
+//    coalesced loads in flight while the current chunk is computed;
+//  * the 4 wave states (max, sum, O^T) are merged in LDS at the end, so one
+//    partial per workgroup reaches HBM.  With a single split the merged row
+//    is written straight to `out` and no combine kernel runs.
+#include "fa_internal.hpp"
+#include "fa_tiles.hpp"
+
+namespace fa {
+
+struct DecodeArgs {
+  const void* q;
+  int64_t q_stride[4];  // batch, head, row, dim
+  void* out;
+  int64_t out_stride[4];
+  const void* k;
+  const void* v;
+  // Contiguous cache: key n of (b, hk) at base + b*s0 + hk*s1 + n*s2.
+  // Paged cache:      key n at base + phys*s0 + (n % bs)*s1 + hk*s2,
+  //                   phys = block_table[b*bt0 + (n / bs)*bt1].
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  const int32_t* block_table;
+  int64_t bt_stride[2];
+  int32_t num_blocks;
+  int32_t block_shift;  // log2(block_size)
+  const int32_t* lens;  // NULL: every sequence has max_len keys
+  int64_t lens_stride;
+  int32_t max_len;      // Sk, or max_blocks * block_size when paged
+  int32_t batch, heads_q, heads_kv, seqlen_q, head_dim;
+  float scale_log2;
+  int32_t num_splits;
+  float* ws_o;          // [splits][B][Hq][Sq][D] fp32
+  float* ws_lse;        // [splits][B][Hq][Sq] fp32
+};
+
+template <typename Tag, int D>
+struct DecCfg {
+  using EL = Elem<Tag>;
+  using S = typename EL::S;
+  static constexpr int NW = (D >= 512) ? 2 : 4;  // 4 wave slots of D=512 exceed 160 KiB
+  static constexpr int NT = 64 * NW;
+  static constexpr int CH = 32;  // keys per wave chunk
+  static constexpr int DO = (D <= 128) ? D : 128;
+  static constexpr bool QREG = D <= 128;
+  static constexpr int KLD = D + EL::CE;
+  static constexpr int VLD = CH + EL::CE;
+  static constexpr int KT = CH * KLD;
+  static constexpr int VT = DO * VLD;
+  static constexpr int WAVE_ELEMS = KT + VT;
+  static constexpr int LOOP_BYTES = NW * WAVE_ELEMS * (int)sizeof(S);
+  static constexpr int OLD = 33;  // merge buffer row stride (floats)
+  static constexpr int MERGE_BYTES = NW * DO * OLD * 4 + 2 * NW * 32 * 4;
+  static constexpr int LDS_BYTES = LOOP_BYTES > MERGE_BYTES ? LOOP_BYTES : MERGE_BYTES;
+  static constexpr int NSTEP = D / EL::KSTEP;
+  static constexpr int NPV = CH / (2 * EL::E);
+  static constexpr int NDB = DO / 32;
+};
+
+size_t decode_workspace_bytes(int batch, int heads_q, int seqlen_q, int head_dim, int num_splits) {
+  const size_t rows = (size_t)num_splits * batch * heads_q * seqlen_q;
+  size_t bytes = rows * (size_t)head_dim * 4 + rows * 4;
+  return (bytes + 255) / 256 * 256;
+}
+
+template <typename Tag, int D, bool PAGED>
+__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
+  using C = DecCfg<Tag, D>;
+  using EL = Elem<Tag>;
+  using S = typename EL::S;
+  using Op = typename EL::Op;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int split = blockIdx.x;
+  const int group = a.heads_q / a.heads_kv;
+  const int rows = group * a.seqlen_q;
+  const int nrb = (rows + 31) / 32;
+  const int y = blockIdx.y;
+  const int rb = y % nrb;
+  const int bhk = y / nrb;
+  const int b = bhk / a.heads_kv, hk = bhk - b * a.heads_kv;
+  const int dc = blockIdx.z;
+
+  int len = a.max_len;
+  if (a.lens) len = min(max(a.lens[b * a.lens_stride], 0), a.max_len);
+  const int nch = (len + C::CH - 1) / C::CH;
+  const int per = nch / a.num_splits, extra = nch % a.num_splits;
+  const int c0 = split * per + min(split, extra);
+  const int cnt = per + (split < extra ? 1 : 0);
+
+  // This lane's packed query row.
+  const int r = rb * 32 + l32;
+  const bool rvalid = r < rows;
+  const int g = rvalid ? r / a.seqlen_q : 0;
+  const int mq = rvalid ? r - g * a.seqlen_q : 0;
+  const int hq = hk * group + g;
+  const S* qrow = reinterpret_cast<const S*>(a.q) + b * a.q_stride[0] + hq * a.q_stride[1] +
+                  mq * a.q_stride[2] + EL::E * h;
+  Op qop[C::QREG ? C::NSTEP : 1];
+  if constexpr (C::QREG) {
+#pragma unroll
+    for (int s = 0; s < C::NSTEP; ++s) qop[s] = rvalid ? load_op<Tag>(qrow + EL::KSTEP * s) : zero_op<Tag>();
+  }
+
+  const S* kbase = reinterpret_cast<const S*>(a.k);
+  const S* vbase = reinterpret_cast<const S*>(a.v);
+  if constexpr (!PAGED) {
+    kbase += b * a.k_stride[0] + hk * a.k_stride[1];
+    vbase += b * a.v_stride[0] + hk * a.v_stride[1];
+  } else {
+    kbase += hk * a.k_stride[2];
+    vbase += hk * a.v_stride[2];
+  }
+  // Offset (elements) of key n's row, or -1 when the key is absent.
+  auto key_off = [&](int n, const int64_t* st) -> int64_t {
+    if (n >= len) return -1;
+    if constexpr (!PAGED) {
+      return (int64_t)n * st[2];
+    } else {
+      const int blk = n >> a.block_shift, pos = n & ((1 << a.block_shift) - 1);
+      const int phys = a.block_table[b * a.bt_stride[0] + blk * a.bt_stride[1]];
+      if (phys < 0 || phys >= a.num_blocks) return -1;
+      return (int64_t)phys * st[0] + (int64_t)pos * st[1];
+    }
+  };
+
+  S* ks = reinterpret_cast<S*>(smem_raw) + wave * C::WAVE_ELEMS;
+  S* vs = ks + C::KT;
+  RowTile<Tag, C::CH, D, 64> kt;
+  TransTile<Tag, C::CH, C::DO, 64> vt;
+  uint32_t valid_next = 0, valid_cur = 0;
+  auto load_chunk = [&](int c) {
+    const int n0 = c * C::CH;
+    kt.load([&](int rr) -> const S* {
+      const int64_t o = key_off(n0 + rr, a.k_stride); return o < 0 ? nullptr : kbase + o; }, lane);
+    vt.load([&](int rr) -> const S* {
+      const int64_t o = key_off(n0 + rr, a.v_stride); return o < 0 ? nullptr : vbase + o + dc * C::DO; }, lane);
+    valid_next = (uint32_t)__ballot(l32 == lane && key_off(n0 + l32, a.k_stride) >= 0);
+  };
+
+  float m_i = kNegInf, l_i = 0.f;
+  f32x16 acc[C::NDB];
+#pragma unroll
+  for (int i = 0; i < C::NDB; ++i) acc[i] = zero16();
+
+  const int rounds = (cnt + C::NW - 1) / C::NW;
+  int my = wave;  // chunk index (relative to c0) of this wave in the current round
+  if (rounds > 0 && my < cnt) load_chunk(c0 + my);
+  for (int it = 0; it < rounds; ++it) {
+    const bool have = my < cnt;
+    if (have) {
+      kt.store(ks, C::KLD, lane);
+      vt.store(vs, C::VLD, lane);
+      valid_cur = valid_next;
+    }
+    __syncthreads();
+    const int nxt = my + C::NW;
+    if (it + 1 < rounds && nxt < cnt) load_chunk(c0 + nxt);
+    if (have) {
+      f32x16 sacc = zero16();
+      const S* krow = ks + l32 * C::KLD + EL::E * h;
+#pragma unroll
+      for (int s = 0; s < C::NSTEP; ++s) {
+        Op bq;
+        if constexpr (C::QREG) bq = qop[s];
+        else bq = rvalid ? load_op<Tag>(qrow + EL::KSTEP * s) : zero_op<Tag>();
+        sacc = EL::mma(load_op<Tag>(krow + EL::KSTEP * s), bq, sacc);
+      }
+      float tmax = kNegInf;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kr = acc_row(i, h);
+        const float x = ((valid_cur >> kr) & 1u) ? sacc[i] * a.scale_log2 : kNegInf;
+        sacc[i] = x;
+        tmax = fmaxf(tmax, x);
+      }
+      tmax = fmaxf(tmax, xor32(tmax));
+      const float m_new = fmaxf(m_i, tmax);
+      const float m_use = (m_new == kNegInf) ? 0.f : m_new;
+      const float alpha = exp2f(m_i - m_use);
+      float rsum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float pv = exp2f(sacc[i] - m_use);
+        sacc[i] = pv;
+        rsum += pv;
+      }
+      rsum += xor32(rsum);
+      l_i = l_i * alpha + rsum;
+      m_i = m_new;
+      constexpr int J = 16 / EL::E;
+      Op pb[C::NPV];
+#pragma unroll
+      for (int j = 0; j < C::NPV; ++j) pb[j] = pack_op<Tag>(sacc, j % J);
+#pragma unroll
+      for (int db = 0; db < C::NDB; ++db) {
+        acc[db] *= alpha;
+        const S* vrow = vs + (db * 32 + l32) * C::VLD;
+#pragma unroll
+        for (int j = 0; j < C::NPV; ++j) acc[db] = EL::mma(lds_op_rowmap<Tag>(vrow, j, h), pb[j], acc[db]);
+      }
+    }
+    __syncthreads();
+    my = nxt;
+  }
+
+  // Merge the 4 wave states of each row through LDS.
+  float* ow = reinterpret_cast<float*>(smem_raw);
+  float* mw = ow + C::NW * C::DO * C::OLD;
+  float* lw = mw + C::NW * 32;
+#pragma unroll
+  for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ow[(wave * C::DO + db * 32 + acc_row(i, h)) * C::OLD + l32] = acc[db][i];
+  if (h == 0) {
+    mw[wave * 32 + l32] = m_i;
+    lw[wave * 32 + l32] = l_i;
+  }
+  __syncthreads();
+
+  for (int idx = tid; idx < 32 * C::DO; idx += C::NT) {
+    const int rr = idx / C::DO, d = idx - (idx / C::DO) * C::DO;
+    const int row = rb * 32 + rr;
+    if (row >= rows) continue;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < C::NW; ++w) M = fmaxf(M, mw[w * 32 + rr]);
+    const float Mu = (M == kNegInf) ? 0.f : M;
+    float L = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < C::NW; ++w) {
+      const float sc = exp2f(mw[w * 32 + rr] - Mu);
+      L += lw[w * 32 + rr] * sc;
+      o += ow[(w * C::DO + d) * C::OLD + rr] * sc;
+    }
+    const float Ls = (L == 0.f) ? 1.f : L;
+    o /= Ls;
+    const int gg = row / a.seqlen_q, mm = row - gg * a.seqlen_q;
+    const int hh = hk * group + gg;
+    const int dd = dc * C::DO + d;
+    if (a.num_splits == 1) {
+      S* op = reinterpret_cast<S*>(a.out) + b * a.out_stride[0] + hh * a.out_stride[1] + mm * a.out_stride[2];
+      op[dd] = EL::from_f(o);
+    } else {
+      const int64_t prow = (((int64_t)split * a.batch + b) * a.heads_q + hh) * a.seqlen_q + mm;
+      a.ws_o[prow * a.head_dim + dd] = o;
+      if (dc == 0 && d == 0) a.ws_lse[prow] = (M == kNegInf || L == 0.f) ? kNegInf : (M + __log2f(L)) * kLn2;
+    }
+  }
+}
+
+// out[row] = sum_s w_s O_s / sum_s w_s,  w_s = exp(lse_s - max lse) (0 for -inf).
+template <typename Tag>
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
+  using EL = Elem<Tag>;
+  using S = typename EL::S;
+  const int rows = a.batch * a.heads_q * a.seqlen_q;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const int64_t plane = (int64_t)rows;
+  float M = kNegInf;
+  for (int s = 0; s < a.num_splits; ++s) M = fmaxf(M, a.ws_lse[s * plane + row]);
+  const float Mu = (M == kNegInf) ? 0.f : M;
+  const int mm = row % a.seqlen_q;
+  const int hh = (row / a.seqlen_q) % a.heads_q;
+  const int bb = row / (a.seqlen_q * a.heads_q);
+  S* op = reinterpret_cast<S*>(a.out) + bb * a.out_stride[0] + hh * a.out_stride[1] + mm * a.out_stride[2];
+  for (int d = lane; d < a.head_dim; d += 64) {
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < a.num_splits; ++s) {
+      const float l = a.ws_lse[s * plane + row];
+      const float w = (l == kNegInf) ? 0.f : __expf(l - Mu);
+      den += w;
+      num += w * a.ws_o[(s * plane + row) * a.head_dim + d];
+    }
+    op[d] = EL::from_f(num / (den == 0.f ? 1.f : den));
+  }
+}
+
+template <typename Tag, int D, bool PAGED>
+static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
+  using C = DecCfg<Tag, D>;
+  auto kern = decode_kernel<Tag, D, PAGED>;
+  hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
+  if (e != hipSuccess) return e;
+  const int group = a.heads_q / a.heads_kv;
+  const int nrb = (group * a.seqlen_q + 31) / 32;
+  dim3 grid(a.num_splits, a.batch * a.heads_kv * nrb, D / C::DO);
+  hipLaunchKernelGGL(kern, grid, dim3(C::NT), C::LDS_BYTES, stream, a);
+  e = hipGetLastError();
+  if (e != hipSuccess || a.num_splits == 1) return e;
+  const int rows = a.batch * a.heads_q * a.seqlen_q;
+  hipLaunchKernelGGL((decode_combine_kernel<Tag>), dim3((rows + 3) / 4), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+template <typename Tag, bool PAGED>
+static hipError_t decode_by_dim(const DecodeArgs& a, hipStream_t s) {
+  switch (a.head_dim) {
+    case 32: return run_decode<Tag, 32, PAGED>(a, s);
+    case 64: return run_decode<Tag, 64, PAGED>(a, s);
+    case 128: return run_decode<Tag, 128, PAGED>(a, s);
+    case 256: return run_decode<Tag, 256, PAGED>(a, s);
+    case 512: return run_decode<Tag, 512, PAGED>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <bool PAGED>
+static hipError_t decode_dispatch(int dtype, const DecodeArgs& a, hipStream_t s) {
+  if (dtype == FA_DTYPE_F16) return decode_by_dim<f16_t, PAGED>(a, s);
+  if (dtype == FA_DTYPE_BF16) return decode_by_dim<bf16_t, PAGED>(a, s);
+  return hipErrorInvalidValue;
+}
+
+static void split_workspace(DecodeArgs& a, void* ws) {
+  const size_t rows = (size_t)a.num_splits * a.batch * a.heads_q * a.seqlen_q;
+  a.ws_o = reinterpret_cast<float*>(ws);
+  a.ws_lse = a.ws_o + rows * a.head_dim;
+}
+
+hipError_t launch_decode(const fa_decode_params& p, hipStream_t s) {
+  DecodeArgs a{};
+  a.q = p.q;
+  for (int i = 0; i < 4; ++i) { a.q_stride[i] = p.q_stride[i]; a.out_stride[i] = p.out_stride[i]; }
+  a.out = p.out;
+  a.k = p.k;
+  a.v = p.v;
+  for (int i = 0; i < 3; ++i) { a.k_stride[i] = p.k_stride[i]; a.v_stride[i] = p.v_stride[i]; }
+  a.lens = p.cache_seqlens;
+  a.lens_stride = p.cache_seqlens_stride;
+  a.max_len = p.seqlen_k;
+  a.batch = p.batch;
+  a.heads_q = p.heads_q;
+  a.heads_kv = p.heads_kv;
+  a.seqlen_q = p.seqlen_q;
+  a.head_dim = p.head_dim;
+  a.scale_log2 = p.softmax_scale * kLog2e;
+  a.num_splits = p.num_splits;
+  split_workspace(a, p.workspace);
+  return decode_dispatch<false>(p.dtype, a, s);
+}
+
+hipError_t launch_paged(const fa_paged_params& p, hipStream_t s) {
+  DecodeArgs a{};
+  a.q = p.q;
+  a.q_stride[0] = p.q_stride[0];
+  a.q_stride[1] = p.q_stride[1];
+  a.q_stride[2] = 0;
+  a.q_stride[3] = p.q_stride[2];
+  a.out = p.out;
+  a.out_stride[0] = p.out_stride[0];
+  a.out_stride[1] = p.out_stride[1];
+  a.out_stride[2] = 0;
+  a.out_stride[3] = p.out_stride[2];
+  a.k = p.k_cache;
+  a.v = p.v_cache;
+  for (int i = 0; i < 3; ++i) { a.k_stride[i] = p.k_stride[i]; a.v_stride[i] = p.v_stride[i]; }
+  a.block_table = p.block_table;
+  a.bt_stride[0] = p.block_table_stride[0];
+  a.bt_stride[1] = p.block_table_stride[1];
+  a.num_blocks = p.num_blocks;
+  int shift = 0;
+  while ((1 << shift) < p.block_size) ++shift;
+  a.block_shift = shift;
+  a.lens = p.context_lens;
+  a.lens_stride = p.context_lens_stride;
+  a.max_len = p.max_blocks * p.block_size;
+  a.batch = p.batch;
+  a.heads_q = p.heads_q;
+  a.heads_kv = p.heads_kv;
+  a.seqlen_q = 1;
+  a.head_dim = p.head_dim;
+  a.scale_log2 = p.softmax_scale * kLog2e;
+  a.num_splits = p.num_splits;
+  split_workspace(a, p.workspace);
+  return decode_dispatch<true>(p.dtype, a, s);
+}
+
+}  // namespace fa

@@ -19,6 +19,8 @@
 // Work order: the m-block index is the slowest-varying grid coordinate and is
 // walked from the last block down, so under causal masking the longest
 // workgroups are dispatched first.
+#include <type_traits>
+
 #include "fa_internal.hpp"
 #include "fa_tiles.hpp"
 
@@ -206,16 +208,32 @@ __global__ __launch_bounds__(256) void fwd_kernel(fa_fwd_params p, int num_m_blo
             }
         }
       }
-      // O^T += V^T P^T.
-      Op pb[C::NPV];
+      // O^T += V^T P^T.  bf16 keeps only 8 mantissa bits, so P is fed as
+      // hi + lo bf16 parts (two MFMAs on the same V^T operand); the product
+      // then carries P to ~2^-17 and the output error is dominated by the
+      // final rounding of O.
+      constexpr bool PSPLIT = std::is_same<Tag, bf16_t>::value;
+      Op pb[C::NPV], pl[PSPLIT ? C::NPV : 1];
       constexpr int J = 16 / EL::E;  // MFMAs per 32-key accumulator block
 #pragma unroll
       for (int j = 0; j < C::NPV; ++j) pb[j] = pack_op<Tag>(sacc[j / J], j % J);
+      if constexpr (PSPLIT) {
+#pragma unroll
+        for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sacc[kb2][i] -= EL::to_f(EL::from_f(sacc[kb2][i]));
+#pragma unroll
+        for (int j = 0; j < C::NPV; ++j) pl[j] = pack_op<Tag>(sacc[j / J], j % J);
+      }
 #pragma unroll
       for (int db = 0; db < C::NDB; ++db) {
         const S* vrow = Vs + (db * 32 + l32) * C::VLD;
 #pragma unroll
-        for (int j = 0; j < C::NPV; ++j) acc[db] = EL::mma(lds_op_rowmap<Tag>(vrow, j, h), pb[j], acc[db]);
+        for (int j = 0; j < C::NPV; ++j) {
+          const Op a = lds_op_rowmap<Tag>(vrow, j, h);
+          acc[db] = EL::mma(a, pb[j], acc[db]);
+          if constexpr (PSPLIT) acc[db] = EL::mma(a, pl[j], acc[db]);
+        }
       }
     }
 

@@ -99,7 +99,7 @@ class TinyParams(ctypes.Structure):
 _STRUCTS = (FwdParams, BwdParams, DecodeParams, PagedParams, TinyParams)
 EXPORTS = (
     "fa_abi_version", "fa_last_error_string", "fa_params_size", "fa_decode_workspace_bytes",
-    "fa_fwd", "fa_bwd", "fa_decode_splitk", "fa_decode_paged", "fa_tiny_fwd_f32",
+    "fa_fwd", "fa_bwd", "fa_bwd_phase", "fa_decode_splitk", "fa_decode_paged", "fa_tiny_fwd_f32",
 )
 
 _lib = None
@@ -136,6 +136,8 @@ def lib():
             fn = getattr(handle, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]
+        handle.fa_bwd_phase.restype = ctypes.c_int
+        handle.fa_bwd_phase.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_int, ctypes.c_void_p]
         if handle.fa_abi_version() != ABI_VERSION:
             raise RuntimeError(f"{_LIB_NAME} ABI {handle.fa_abi_version()} != binding ABI {ABI_VERSION}")
         for which, struct in enumerate(_STRUCTS):
@@ -165,6 +167,10 @@ def call(name, params, device_tensor):
     """Invoke an fa_* entry point on the current stream of the tensor's device."""
     fn = getattr(lib(), name)
     _check(fn(ctypes.byref(params), _stream(device_tensor)), name)
+
+
+def call_bwd_phase(params, phase, device_tensor):
+    _check(lib().fa_bwd_phase(ctypes.byref(params), int(phase), _stream(device_tensor)), "fa_bwd_phase")
 
 
 def decode_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits):

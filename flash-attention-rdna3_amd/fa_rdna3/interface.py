@@ -218,8 +218,10 @@ def _forward(query, key, value, causal, softmax_scale, window, softcap, bias, al
     return out, lse
 
 
-def _backward(dout, query, key, value, out, lse, causal, softmax_scale, window, softcap, bias, alibi,
-              dropout_p, dropout_seed):
+def _bwd_setup(dout, query, key, value, out, lse, causal, softmax_scale, window, softcap, bias, alibi,
+               dropout_p, dropout_seed):
+    """Allocate dq/dk/dv/delta and fill fa_bwd_params for the dense backward.
+    Returns (params, dq, dk, dv, tensors kept alive for the launch)."""
     batch, heads, seqlen_q, head_dim = query.shape
     seqlen_k = key.shape[2]
     kdim = _kernel_head_dim(head_dim)
@@ -241,10 +243,33 @@ def _backward(dout, query, key, value, out, lse, causal, softmax_scale, window, 
     for name, t in (("dout_stride", do), ("dq_stride", dq), ("dk_stride", dk), ("dv_stride", dv)):
         _set(getattr(params, name), _native.strides(t))
     _set(params.delta_stride, [s if n > 1 else 0 for s, n in zip(delta.stride(), delta.shape)])
+    keep = (q, k, v, o, do, lse, delta, bias_t, alibi_t)
+    return params, dq, dk, dv, keep
+
+
+def _backward(dout, query, key, value, out, lse, causal, softmax_scale, window, softcap, bias, alibi,
+              dropout_p, dropout_seed):
+    head_dim = query.shape[-1]
+    params, dq, dk, dv, _keep = _bwd_setup(dout, query, key, value, out, lse, causal, softmax_scale,
+                                           window, softcap, bias, alibi, dropout_p, dropout_seed)
     _native.call("fa_bwd", params, query)
-    if kdim != head_dim:
+    if dq.shape[-1] != head_dim:
         dq, dk, dv = dq[..., :head_dim], dk[..., :head_dim], dv[..., :head_dim]
     return dq, dk, dv
+
+
+def _backward_launcher(dout, query, key, value, out, lse, causal, softmax_scale, window, softcap, bias,
+                       alibi, dropout_p, dropout_seed):
+    """Profiling aid: returns launch(phase) running one backward kernel
+    (0 delta, 1 dK/dV, 2 dQ) on the current stream with fixed buffers."""
+    params, dq, dk, dv, keep = _bwd_setup(dout, query, key, value, out, lse, causal, softmax_scale,
+                                          window, softcap, bias, alibi, dropout_p, dropout_seed)
+
+    def launch(phase):
+        _native.call_bwd_phase(params, phase, query)
+        return dq, dk, dv, keep
+
+    return launch
 
 
 @torch.library.custom_op("fa_rdna3::flash_fwd", mutates_args=())

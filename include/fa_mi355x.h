@@ -234,6 +234,11 @@ size_t fa_decode_workspace_bytes(int batch, int heads_q, int seqlen_q,
 
 int fa_fwd(const fa_fwd_params* params, void* stream);
 int fa_bwd(const fa_bwd_params* params, void* stream);
+/* One stage of fa_bwd: 0 = delta, 1 = dK/dV, 2 = dQ (1 and 2 read delta).
+ * No counterpart in the reference (its three backward launches are separate
+ * Triton calls, interface.py:226/:236/:258); it exists so profilers and
+ * benchmarks can time each backward kernel on its own. */
+int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream);
 int fa_decode_splitk(const fa_decode_params* params, void* stream);
 int fa_decode_paged(const fa_paged_params* params, void* stream);
 int fa_tiny_fwd_f32(const fa_tiny_params* params, void* stream);

@@ -1,0 +1,80 @@
+"""The C-ABI library loads on a CPU host, exports every entry point the
+public header declares, and agrees with the ctypes binding on struct layouts
+(no compute calls: those need a GPU)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from fa_rdna3 import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fa_mi355x.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(fa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_binding_exports():
+    assert set(_declared_functions()) == set(_native.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _native.library_path()], capture_output=True, text=True)
+    if out.returncode == 0:
+        for name in _declared_functions():
+            assert re.search(rf"\bT {name}\b", out.stdout), name
+
+
+def test_abi_version_and_struct_layouts():
+    lib = _native.lib()
+    assert lib.fa_abi_version() == _native.ABI_VERSION
+    for which, struct in enumerate(_native._STRUCTS):
+        assert lib.fa_params_size(which) == ctypes.sizeof(struct), struct.__name__
+    assert lib.fa_params_size(99) == 0
+
+
+def test_workspace_size():
+    # splits * B * H * Sq * (D + 1) fp32, rounded up to 256 bytes
+    n = _native.decode_workspace_bytes(4, 32, 1, 128, 8)
+    assert n == (8 * 4 * 32 * 1 * 129 * 4 + 255) // 256 * 256
+    assert _native.decode_workspace_bytes(0, 32, 1, 128, 8) == 0
+
+
+def test_null_params_are_rejected_without_touching_a_gpu():
+    lib = _native.lib()
+    assert lib.fa_fwd(None, None) == 1
+    assert b"NULL" in lib.fa_last_error_string()
+    assert lib.fa_bwd_phase(None, 5, None) == 1
+
+
+def test_bad_arguments_are_rejected_before_launch():
+    lib = _native.lib()
+    p = _native.FwdParams()
+    p.abi_version = 99
+    assert lib.fa_fwd(ctypes.byref(p), None) == 1
+    assert b"abi_version" in lib.fa_last_error_string()
+    p.abi_version = _native.ABI_VERSION
+    p.dtype, p.head_dim = 0, 48
+    assert lib.fa_fwd(ctypes.byref(p), None) == 2
+    assert b"head_dim" in lib.fa_last_error_string()
+    p.head_dim, p.batch, p.heads_q, p.heads_kv, p.seqlen_q, p.seqlen_k = 64, 1, 6, 4, 8, 8
+    assert lib.fa_fwd(ctypes.byref(p), None) == 1
+    t = _native.TinyParams()
+    t.abi_version, t.seqlen = _native.ABI_VERSION, 33
+    assert lib.fa_tiny_fwd_f32(ctypes.byref(t), None) == 1
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_native, "_LIB_PATH", str(tmp_path / "absent.so"))
+    monkeypatch.setattr(_native, "_lib", None)
+    with pytest.raises(RuntimeError, match="native library not found"):
+        _native.lib()

@@ -1,0 +1,358 @@
+"""torch.library registration, torch.compile, the tiny fp32 op, dropout and
+the SDPA override on the GPU (behaviour contract of the reference tests
+test_torch_library.py, test_tiny.py, test_dropout.py, test_sdpa_dispatch.py)."""
+
+import math
+import threading
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import fa_rdna3.sdpa as sdpa_mod
+from fa_rdna3 import (disable_rdna3_flash_attention, enable_rdna3_flash_attention, flash_attention,
+                      use_rdna3_flash_attention)
+from fa_rdna3.interface import _backward, _can_use_tiny_forward, _forward
+
+pytestmark = pytest.mark.gpu
+DEVICE = "cuda"
+HEADS, HEAD_DIM = 8, 128
+
+
+def test_opcheck_flash_fwd():
+    q = torch.randn(2, 4, 128, 64, device=DEVICE, dtype=torch.float16, requires_grad=True)
+    k, v = torch.randn_like(q), torch.randn_like(q)
+    args = (q, k, v, True, 1.0 / math.sqrt(64), -1, -1, 0.0, None, None, 0.0, 0)
+    torch.library.opcheck(torch.ops.fa_rdna3.flash_fwd, args,
+                          test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
+
+
+def test_torch_compile_matches_eager():
+    q = torch.randn(2, 4, 256, 64, device=DEVICE, dtype=torch.float16, requires_grad=True)
+    k, v = torch.randn_like(q), torch.randn_like(q)
+
+    def f(q, k, v):
+        return flash_attention(q, k, v, causal=True, softmax_scale=0.125).square().sum()
+
+    eager = f(q, k, v)
+    eager.backward()
+    eager_dq = q.grad.clone()
+    q.grad = None
+    compiled = torch.compile(f, fullgraph=True)(q, k, v)
+    compiled.backward()
+    torch.testing.assert_close(compiled, eager, atol=2e-3, rtol=2e-3)
+    torch.testing.assert_close(q.grad, eager_dq, atol=2e-3, rtol=2e-3)
+    torch._dynamo.reset()
+
+
+def _packed(seq):
+    packed = torch.randn(2, seq, 3, HEADS, HEAD_DIM, device=DEVICE)
+    return tuple(t.transpose(1, 2) for t in packed.unbind(2))
+
+
+def _tiny_ref(q, k, v, bias=None):
+    s = torch.matmul(q, k.transpose(-1, -2)) / math.sqrt(HEAD_DIM)
+    if bias is not None:
+        s = s + bias
+    return torch.matmul(torch.softmax(s, dim=-1).nan_to_num(), v)
+
+
+@pytest.mark.parametrize("seq", [1, 6, 19, 32])
+@pytest.mark.parametrize("bias_kind", ["none", "broadcast", "full", "masked_row"])
+def test_tiny_fp32(seq, bias_kind):
+    torch.manual_seed(seq)
+    q, k, v = _packed(seq)
+    bias = None
+    if bias_kind == "broadcast":
+        bias = torch.randn(2, 1, 1, seq, device=DEVICE)
+    elif bias_kind != "none":
+        bias = torch.randn(2, HEADS, seq, seq, device=DEVICE)
+        if bias_kind == "masked_row":
+            bias[:, :, seq // 2, :] = float("-inf")
+    out = flash_attention(q, k, v, bias=bias)
+    assert (out - _tiny_ref(q, k, v, bias)).abs().max().item() < 2e-6
+
+
+@pytest.mark.parametrize("has_bias", [False, True])
+def test_tiny_op_opcheck(has_bias):
+    q, k, v = _packed(6)
+    bias = torch.randn(2, 1, 1, 6, device=DEVICE) if has_bias else None
+    torch.library.opcheck(torch.ops.fa_rdna3.flash_tiny_fwd.default, (q, k, v, 1.0 / math.sqrt(HEAD_DIM), bias, 8))
+
+
+def test_tiny_route_is_inference_only():
+    q, k, v = _packed(19)
+    opts = (False, (-1, -1), 0.0, None, 0.0, HEAD_DIM)
+    assert _can_use_tiny_forward(q, k, v, *opts)
+    q.requires_grad_(True)
+    assert not _can_use_tiny_forward(q, k, v, *opts)
+    q.requires_grad_(False)
+    assert not _can_use_tiny_forward(q.half(), k.half(), v.half(), *opts)
+    assert not _can_use_tiny_forward(q, k, v, True, (-1, -1), 0.0, None, 0.0, HEAD_DIM)
+    assert not _can_use_tiny_forward(q, k, v, False, (-1, -1), 0.0, None, 0.0, 64)
+    assert not _can_use_tiny_forward(*_packed(33), *opts)
+    assert not _can_use_tiny_forward(q, k[:, :, :-1], v[:, :, :-1], *opts)
+    assert not _can_use_tiny_forward(q, k[:, :4], v[:, :4], *opts)
+    assert not _can_use_tiny_forward(q, k, v, False, (4, 0), 0.0, None, 0.0, HEAD_DIM)
+    assert not _can_use_tiny_forward(q, k, v, False, (-1, -1), 10.0, None, 0.0, HEAD_DIM)
+    assert not _can_use_tiny_forward(q, k, v, False, (-1, -1), 0.0, torch.zeros(HEADS, device=DEVICE), 0.0, HEAD_DIM)
+    assert not _can_use_tiny_forward(q, k, v, False, (-1, -1), 0.0, None, 0.1, HEAD_DIM)
+
+
+def test_sdpa_compile_matches_stock_for_tiny_shapes():
+    original = F.scaled_dot_product_attention
+
+    def attn(packed, mask):
+        q, k, v = (t.transpose(1, 2) for t in packed.unbind(2))
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+
+    enable_rdna3_flash_attention()
+    try:
+        compiled = torch.compile(attn, fullgraph=True, dynamic=False)
+        for seq in (5, 6, 19):
+            packed = torch.randn(2, seq, 3, HEADS, HEAD_DIM, device=DEVICE)
+            mask = torch.randn(2, 1, 1, seq, device=DEVICE)
+            q, k, v = (t.transpose(1, 2) for t in packed.unbind(2))
+            expected = original(q, k, v, attn_mask=mask)
+            assert (compiled(packed, mask) - expected).abs().max().item() < 2e-6
+    finally:
+        disable_rdna3_flash_attention()
+        torch._dynamo.reset()
+
+
+def test_compiled_dispatch_preserves_active_bypass():
+    q = torch.randn(1, 1, 6, HEAD_DIM, device=DEVICE)
+    saved = sdpa_mod._original_sdpa
+    sdpa_mod._original_sdpa = lambda q_, k_, v_, **kw: q_ + 1.0
+    try:
+        compiled = torch.compile(sdpa_mod._dispatch_sdpa, fullgraph=True, dynamic=False)
+        with sdpa_mod._bypass_rdna3_flash_attention():
+            torch.testing.assert_close(compiled(q, q, q), q + 1.0)
+    finally:
+        sdpa_mod._original_sdpa = saved
+        torch._dynamo.reset()
+
+
+def test_bypass_in_another_thread_does_not_leak():
+    q = torch.randn(1, 1, 6, HEAD_DIM, device=DEVICE)
+    entered, release = threading.Event(), threading.Event()
+
+    def hold():
+        with sdpa_mod._bypass_rdna3_flash_attention():
+            entered.set()
+            release.wait(timeout=30)
+
+    t = threading.Thread(target=hold)
+    t.start()
+    assert entered.wait(timeout=5)
+    saved = sdpa_mod._original_sdpa
+    sdpa_mod._original_sdpa = lambda q_, k_, v_, **kw: q_ + 1.0
+    try:
+        compiled = torch.compile(sdpa_mod._dispatch_sdpa, fullgraph=True, dynamic=False)
+        torch.testing.assert_close(compiled(q, q, q), flash_attention(q, q, q))
+    finally:
+        release.set()
+        t.join(timeout=5)
+        sdpa_mod._original_sdpa = saved
+        torch._dynamo.reset()
+
+
+def test_dropout_p0_matches_no_dropout():
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(2, 4, 512, 64, device=DEVICE, dtype=torch.float16) for _ in range(3))
+    torch.testing.assert_close(flash_attention(q, k, v, causal=True),
+                               flash_attention(q, k, v, causal=True, dropout_p=0.0))
+
+
+def test_dropout_forward_unbiased():
+    torch.manual_seed(1)
+    q, k, v = (torch.randn(1, 4, 256, 64, device=DEVICE, dtype=torch.float16) for _ in range(3))
+    ref = flash_attention(q, k, v).float()
+    acc = torch.zeros_like(ref)
+    for _ in range(400):
+        acc += flash_attention(q, k, v, dropout_p=0.25).float()
+    assert (acc / 400 - ref).abs().mean().item() < 5e-3
+
+
+def test_dropout_keep_rate():
+    # With v = 1 everywhere, each output element is sum_j keep_j p_j / (1-p):
+    # its mean over rows estimates 1 and its spread reflects the keep rate.
+    torch.manual_seed(3)
+    q = torch.zeros(1, 2, 512, 64, device=DEVICE, dtype=torch.float16)
+    v = torch.ones(1, 2, 512, 64, device=DEVICE, dtype=torch.float16)
+    out = flash_attention(q, q, v, dropout_p=0.3).float()
+    assert abs(out.mean().item() - 1.0) < 0.01
+
+
+def test_dropout_backward_consistency():
+    torch.manual_seed(2)
+    seed, p, scale = 777, 0.2, 0.125
+    q, k, v, do = (torch.randn(1, 2, 128, 64, device=DEVICE, dtype=torch.float16) for _ in range(4))
+    out, lse = _forward(q, k, v, False, scale, (-1, -1), 0.0, None, None, p, seed)
+    dq, dk, dv = _backward(do, q, k, v, out, lse, False, scale, (-1, -1), 0.0, None, None, p, seed)
+    base = (out.float() * do.float()).sum()
+    eps = 0.1
+    for grad, name in ((dq, "q"), (dk, "k"), (dv, "v")):
+        direction = torch.randn_like(q)
+        t = {"q": q, "k": k, "v": v}
+        t[name] = t[name] + eps * direction
+        out2, _ = _forward(t["q"], t["k"], t["v"], False, scale, (-1, -1), 0.0, None, None, p, seed)
+        fd = ((out2.float() * do.float()).sum() - base) / eps
+        analytical = (grad.float() * direction.float()).sum()
+        assert (fd - analytical).abs() / (analytical.abs() + 1.0) < 0.1, name
+
+
+def test_dispatch_matches_reference_and_restores():
+    q, k, v = (torch.randn(2, 8, 1024, 128, device=DEVICE, dtype=torch.float16) for _ in range(3))
+    original = F.scaled_dot_product_attention
+    baseline = original(q, k, v, is_causal=True)
+    enable_rdna3_flash_attention()
+    try:
+        out = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    finally:
+        disable_rdna3_flash_attention()
+    assert F.scaled_dot_product_attention is original
+    torch.testing.assert_close(out.float(), baseline.float(), atol=3e-3, rtol=3e-3)
+
+
+def test_dispatch_routes_decode():
+    q = torch.randn(1, 8, 1, 128, device=DEVICE, dtype=torch.float16)
+    k = torch.randn(1, 8, 8192, 128, device=DEVICE, dtype=torch.float16)
+    v = torch.randn_like(k)
+    ref = F.scaled_dot_product_attention(q, k, v)
+    calls = {"n": 0}
+    real = sdpa_mod.flash_attention_decode
+
+    def spy(*a, **kw):
+        calls["n"] += 1
+        return real(*a, **kw)
+
+    sdpa_mod.flash_attention_decode = spy
+    try:
+        with use_rdna3_flash_attention(), torch.no_grad():
+            out = F.scaled_dot_product_attention(q, k, v)
+    finally:
+        sdpa_mod.flash_attention_decode = real
+    assert calls["n"] == 1
+    torch.testing.assert_close(out.float(), ref.float(), atol=3e-3, rtol=3e-3)
+
+
+def test_dispatch_routes_attn_mask():
+    torch.manual_seed(2)
+    q, k, v = (torch.randn(2, 4, 256, 64, device=DEVICE, dtype=torch.float16) for _ in range(3))
+    mask = torch.randn(2, 4, 256, 256, device=DEVICE, dtype=torch.float16)
+    ref = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+    with use_rdna3_flash_attention():
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+    torch.testing.assert_close(out.float(), ref.float(), atol=3e-3, rtol=3e-3)
+
+
+def test_dispatch_bool_mask():
+    torch.manual_seed(4)
+    q, k, v = (torch.randn(1, 4, 128, 64, device=DEVICE, dtype=torch.float16) for _ in range(3))
+    mask = torch.rand(1, 1, 128, 128, device=DEVICE) < 0.7
+    mask |= torch.eye(128, device=DEVICE, dtype=torch.bool)
+    ref = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+    with use_rdna3_flash_attention():
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+    torch.testing.assert_close(out.float(), ref.float(), atol=3e-3, rtol=3e-3)
+
+
+def test_dispatch_falls_back_for_unsupported_head_dim():
+    q, k, v = (torch.randn(1, 4, 256, 640, device=DEVICE, dtype=torch.float16) for _ in range(3))
+    ref = F.scaled_dot_product_attention(q, k, v)
+    with use_rdna3_flash_attention():
+        out = F.scaled_dot_product_attention(q, k, v)
+    torch.testing.assert_close(out.float(), ref.float(), atol=3e-3, rtol=3e-3)
+
+
+def test_dispatch_preserves_pytorch_causal_cross_alignment():
+    q = torch.zeros(1, 1, 1, 16, device=DEVICE, dtype=torch.float16)
+    k = torch.zeros(1, 1, 3, 16, device=DEVICE, dtype=torch.float16)
+    v = torch.tensor([1.0, 2.0, 4.0], device=DEVICE, dtype=torch.float16).view(1, 1, 3, 1).expand_as(k).contiguous()
+    ref = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    with use_rdna3_flash_attention():
+        out = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    torch.testing.assert_close(out, ref)
+
+
+def test_dispatch_defers_causal_with_mask_to_original():
+    """attn_mask together with is_causal is never taken by the kernels; the
+    original SDPA decides (it raises on some torch builds, not on others)."""
+    q = torch.randn(1, 1, 4, 16, device=DEVICE, dtype=torch.float16)
+    mask = torch.ones(4, 4, device=DEVICE, dtype=torch.bool)
+    original = F.scaled_dot_product_attention
+    try:
+        expected, expected_exc = original(q, q, q, attn_mask=mask, is_causal=True), None
+    except RuntimeError as exc:
+        expected, expected_exc = None, type(exc)
+    calls = {"n": 0}
+    with use_rdna3_flash_attention():
+        real = sdpa_mod._original_sdpa
+
+        def spy(*a, **kw):
+            calls["n"] += 1
+            return real(*a, **kw)
+
+        sdpa_mod._original_sdpa = spy
+        try:
+            if expected_exc is not None:
+                with pytest.raises(expected_exc):
+                    F.scaled_dot_product_attention(q, q, q, attn_mask=mask, is_causal=True)
+            else:
+                out = F.scaled_dot_product_attention(q, q, q, attn_mask=mask, is_causal=True)
+                torch.testing.assert_close(out, expected)
+        finally:
+            sdpa_mod._original_sdpa = real
+    assert calls["n"] == 1
+
+
+def test_dispatch_defers_tiny_sequence_in_training():
+    tiny = lambda: torch.randn(1, 8, 12, 128, device=DEVICE, dtype=torch.float16, requires_grad=True)
+    big = torch.randn(2, 8, 512, 128, device=DEVICE, dtype=torch.float16, requires_grad=True)
+    enable_rdna3_flash_attention()
+    real = sdpa_mod._original_sdpa
+    calls = {"n": 0}
+
+    def spy(*a, **kw):
+        calls["n"] += 1
+        return real(*a, **kw)
+
+    sdpa_mod._original_sdpa = spy
+    try:
+        F.scaled_dot_product_attention(tiny(), tiny(), tiny(), is_causal=True)
+        assert calls["n"] == 1
+        with torch.no_grad():
+            F.scaled_dot_product_attention(tiny(), tiny(), tiny(), is_causal=True)
+        assert calls["n"] == 1
+        F.scaled_dot_product_attention(big, big, big, is_causal=True)
+        assert calls["n"] == 1
+    finally:
+        sdpa_mod._original_sdpa = real
+        disable_rdna3_flash_attention()
+
+
+def test_dispatch_respects_enable_gqa():
+    q = torch.randn(1, 4, 64, 64, device=DEVICE, dtype=torch.float16)
+    k = torch.randn(1, 2, 64, 64, device=DEVICE, dtype=torch.float16)
+    v = torch.randn_like(k)
+    with use_rdna3_flash_attention():
+        with pytest.raises(RuntimeError):
+            F.scaled_dot_product_attention(q, k, v)
+        out = F.scaled_dot_product_attention(q, k, v, enable_gqa=True)
+    ref = F.scaled_dot_product_attention(q, k, v, enable_gqa=True)
+    torch.testing.assert_close(out.float(), ref.float(), atol=3e-3, rtol=3e-3)
+
+
+def test_dispatch_uses_decode_for_inference_tensors_with_grad_enabled():
+    q = torch.randn(1, 8, 1, 128, device=DEVICE, dtype=torch.float16)
+    k = torch.randn(1, 8, 2048, 128, device=DEVICE, dtype=torch.float16)
+    calls = {"n": 0}
+    real = sdpa_mod.flash_attention_decode
+    sdpa_mod.flash_attention_decode = lambda *a, **kw: (calls.__setitem__("n", calls["n"] + 1), real(*a, **kw))[1]
+    try:
+        with use_rdna3_flash_attention():
+            F.scaled_dot_product_attention(q, k, torch.randn_like(k))
+    finally:
+        sdpa_mod.flash_attention_decode = real
+    assert calls["n"] == 1
