@@ -267,7 +267,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip decode/varlen side measurements")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 10 device copies of MIB MiB (scales rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        n = args.copy_calibration * 1024 * 1024
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 10}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: the attention path is single-GPU in this build "
               "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)

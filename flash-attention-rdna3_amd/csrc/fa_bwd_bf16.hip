@@ -1,0 +1,6 @@
+// Instantiates the bwd kernels for bf16.
+#include "fa_bwd_impl.hpp"
+
+namespace fa {
+template hipError_t bwd_by_mods<bf16_t>(const fa_bwd_params& p, int ph, hipStream_t s);
+}  // namespace fa

@@ -150,6 +150,12 @@ __device__ inline typename Elem<Tag>::Op lds_op_rowmap(const typename Elem<Tag>:
   }
 }
 
+// s_waitcnt vmcnt(0) (gfx9 encoding: expcnt/lgkmcnt fields left at "no wait").
+// Used once after the register operands loaded before a main loop, so the
+// compiler's wait analysis knows they are resident on every path into the
+// loop and does not drain the in-flight prefetches at the first MFMA.
+__device__ inline void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // ---------------------------------------------------------------------------
 // Cross-lane helpers (wave64).
 // ---------------------------------------------------------------------------

@@ -90,7 +90,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   using Op = typename EL::Op;
   extern __shared__ __align__(16) unsigned char smem_raw[];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int h = lane >> 5, l32 = lane & 31;
   const int split = blockIdx.x;
   const int group = a.heads_q / a.heads_kv;
@@ -121,6 +122,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   if constexpr (C::QREG) {
 #pragma unroll
     for (int s = 0; s < C::NSTEP; ++s) qop[s] = rvalid ? load_op<Tag>(qrow + EL::KSTEP * s) : zero_op<Tag>();
+    wait_vm_all();
   }
 
   const S* kbase = reinterpret_cast<const S*>(a.k);
@@ -153,9 +155,9 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   auto load_chunk = [&](int c) {
     const int n0 = c * C::CH;
     kt.load([&](int rr) -> const S* {
-      const int64_t o = key_off(n0 + rr, a.k_stride); return o < 0 ? nullptr : kbase + o; }, lane);
+      const int64_t o = key_off(n0 + rr, a.k_stride); return o < 0 ? nullptr : kbase + o; }, kbase, lane);
     vt.load([&](int rr) -> const S* {
-      const int64_t o = key_off(n0 + rr, a.v_stride); return o < 0 ? nullptr : vbase + o + dc * C::DO; }, lane);
+      const int64_t o = key_off(n0 + rr, a.v_stride); return o < 0 ? nullptr : vbase + o + dc * C::DO; }, vbase + dc * C::DO, lane);
     valid_next = (uint32_t)__ballot(l32 == lane && key_off(n0 + l32, a.k_stride) >= 0);
   };
 

@@ -10,11 +10,23 @@
 //               when the contracted index is the tile's row (P.V, dS^T.Q ...).
 //               Each thread loads 4 consecutive rows of one chunk and writes
 //               4-row runs, so LDS writes are 8 (16-bit) or 16 (fp32) bytes.
+// Loads are unconditional: an absent row reads a known-valid fallback
+// address and is zeroed by a select when the registers go to LDS.  Keeping
+// branches off the load path lets every load of a tile stay in flight while
+// the previous tile is computed (a branch around a load forces the compiler
+// to drain the memory counter at the join).
 #pragma once
 
 #include "fa_common.hpp"
 
 namespace fa {
+
+// x if keep else 0, component-wise (a whole-struct select defeats register
+// promotion of the staging arrays).
+__device__ inline uint4 masked(const uint4& x, uint32_t keep) {
+  const uint32_t m = 0u - keep;
+  return make_uint4(x.x & m, x.y & m, x.z & m, x.w & m);
+}
 
 template <typename Tag, int R, int COLS, int NT>
 struct RowTile {
@@ -25,19 +37,20 @@ struct RowTile {
   static constexpr int CH = R * CPR;
   static constexpr int PT = (CH + NT - 1) / NT;
   uint4 r[PT];
+  uint32_t ok;
 
   // rowptr(row) returns the address of element 0 of that tile row, or nullptr
-  // for a zero row.
+  // for a zero row; `fallback` is any readable row of the same tensor.
   template <typename RowPtr>
-  __device__ inline void load(RowPtr rowptr, int tid) {
+  __device__ inline void load(RowPtr rowptr, const S* fallback, int tid) {
+    ok = 0;
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
       const int c = tid + NT * j;
-      r[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (CH % NT == 0 || c < CH) {
-        const S* p = rowptr(c / CPR);
-        if (p) r[j] = *reinterpret_cast<const uint4*>(p + (c % CPR) * CE);
-      }
+      const S* p = (CH % NT == 0 || c < CH) ? rowptr(c / CPR) : nullptr;
+      ok |= (p != nullptr ? 1u : 0u) << j;
+      p = p ? p : fallback;
+      r[j] = *reinterpret_cast<const uint4*>(p + (c % CPR) * CE);
     }
   }
   __device__ inline void store(S* lds, int LD, int tid) const {
@@ -45,7 +58,7 @@ struct RowTile {
     for (int j = 0; j < PT; ++j) {
       const int c = tid + NT * j;
       if (CH % NT == 0 || c < CH)
-        *reinterpret_cast<uint4*>(lds + (c / CPR) * LD + (c % CPR) * CE) = r[j];
+        *reinterpret_cast<uint4*>(lds + (c / CPR) * LD + (c % CPR) * CE) = masked(r[j], (ok >> j) & 1u);
     }
   }
 };
@@ -58,22 +71,23 @@ struct TransTile {
   static constexpr int CPR = COLS / CE;
   static constexpr int ITEMS = (R / 4) * CPR;  // (row quad, chunk)
   static constexpr int PT = (ITEMS + NT - 1) / NT;
-  uint4 r[PT][4];
+  uint4 r[PT * 4];  // flat: (item j, row q) at 4*j + q
+  uint32_t ok;
 
   template <typename RowPtr>
-  __device__ inline void load(RowPtr rowptr, int tid) {
+  __device__ inline void load(RowPtr rowptr, const S* fallback, int tid) {
+    ok = 0;
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
       const int it = tid + NT * j;
+      const bool in = ITEMS % NT == 0 || it < ITEMS;
+      const int rq = it / CPR, cc = it % CPR;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) r[j][q] = make_uint4(0u, 0u, 0u, 0u);
-      if (ITEMS % NT == 0 || it < ITEMS) {
-        const int rq = it / CPR, cc = it % CPR;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const S* p = rowptr(4 * rq + q);
-          if (p) r[j][q] = *reinterpret_cast<const uint4*>(p + cc * CE);
-        }
+      for (int q = 0; q < 4; ++q) {
+        const S* p = in ? rowptr(4 * rq + q) : nullptr;
+        ok |= (p != nullptr ? 1u : 0u) << (4 * j + q);
+        p = p ? p : fallback;
+        r[4 * j + q] = *reinterpret_cast<const uint4*>(p + cc * CE);
       }
     }
   }
@@ -83,31 +97,33 @@ struct TransTile {
       const int it = tid + NT * j;
       if (ITEMS % NT == 0 || it < ITEMS) {
         const int rq = it / CPR, cc = it % CPR;
+        uint4 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = masked(r[4 * j + q], (ok >> (4 * j + q)) & 1u);
         if constexpr (sizeof(S) == 2) {
-          const uint16_t* v0 = reinterpret_cast<const uint16_t*>(&r[j][0]);
-          const uint16_t* v1 = reinterpret_cast<const uint16_t*>(&r[j][1]);
-          const uint16_t* v2 = reinterpret_cast<const uint16_t*>(&r[j][2]);
-          const uint16_t* v3 = reinterpret_cast<const uint16_t*>(&r[j][3]);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
+            // element e of each row sits in dword e/2, low half if e even
+            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
             uint2 w;
-            w.x = (uint32_t)v0[e] | ((uint32_t)v1[e] << 16);
-            w.y = (uint32_t)v2[e] | ((uint32_t)v3[e] << 16);
+            w.x = __builtin_amdgcn_perm(word(v[1], e >> 1), word(v[0], e >> 1), sel);
+            w.y = __builtin_amdgcn_perm(word(v[3], e >> 1), word(v[2], e >> 1), sel);
             *reinterpret_cast<uint2*>(lds + (cc * CE + e) * LD + 4 * rq) = w;
           }
         } else {
-          const uint32_t* v0 = reinterpret_cast<const uint32_t*>(&r[j][0]);
-          const uint32_t* v1 = reinterpret_cast<const uint32_t*>(&r[j][1]);
-          const uint32_t* v2 = reinterpret_cast<const uint32_t*>(&r[j][2]);
-          const uint32_t* v3 = reinterpret_cast<const uint32_t*>(&r[j][3]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            uint4 w = make_uint4(v0[e], v1[e], v2[e], v3[e]);
+            uint4 w = make_uint4(word(v[0], e), word(v[1], e), word(v[2], e), word(v[3], e));
             *reinterpret_cast<uint4*>(lds + (cc * CE + e) * LD + 4 * rq) = w;
           }
         }
       }
     }
+  }
+
+ private:
+  __device__ static inline uint32_t word(const uint4& u, int k) {
+    return k == 0 ? u.x : k == 1 ? u.y : k == 2 ? u.z : u.w;
   }
 };
 
