@@ -169,7 +169,7 @@ def dkdv_roofline(tensors, iters=50):
     fwd, _ = cfg2_flops()
     flops = 2.0 * fwd  # S recompute, dP, dV, dK: 4 of the 5 algorithmic backward GEMMs
     achieved = flops / (ms * 1e-3) / 1e12
-    return {"kernel": "bwd_dkdv_kernel<f16,128>", "bound": "mfma", "achieved": round(achieved, 2),
+    return {"kernel": "dkdv16_kernel<f16,128,0>", "bound": "mfma", "achieved": round(achieved, 2),
             "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
             "traffic": None, "avg_us": round(ms * 1e3, 2), "flops_per_launch": flops}
 

@@ -1,0 +1,418 @@
+// fa_bwd16.hpp - dK/dV and dQ kernels specialised for 16-bit inputs, D <= 128.
+//
+// Same math as bwd_dkdv_kernel / bwd_dq_kernel (reference
+// kernels/backward.py:49-322, _common.py:347-508), with the gfx950 layout of
+// fa_fwd16.hpp:
+//  * every LDS tile is row-major with an XOR chunk swizzle; operands that
+//    contract over the tile row (dO^T, Q^T for dK/dV; K^T for dQ) are read
+//    with ds_read_b64_tr_b16 from the same row-major tile that feeds the
+//    row-contracting MFMAs, so each tile is loaded and stored once;
+//  * blocks strictly inside the visible region skip the per-score masking;
+//  * LSE is staged as lse*log2(e), with +inf for rows that must contribute
+//    nothing (past the sequence end, or no visible key), so
+//    P = exp2(s*c - lse2) is 0 there without a select.
+#pragma once
+
+#include "fa_internal.hpp"
+#include "fa_tiles.hpp"
+
+namespace fa {
+
+__device__ inline float lse2_of(float lse) { return lse == kNegInf ? __builtin_inff() : lse * kLog2e; }
+
+// ---------------------------------------------------------------------------
+// dK / dV: each wave owns 32 keys (lane axis of S = Q K^T).
+// ---------------------------------------------------------------------------
+template <int D>
+struct Dkdv16Cfg {
+  static constexpr int NW = 4;
+  static constexpr int NT = 64 * NW;
+  static constexpr int BN = 32 * NW;
+  static constexpr int BMQ = 32;
+  static constexpr int QT = BMQ * D;                    // elements per Q / dO tile
+  static constexpr int STAGE_BYTES = 2 * QT * 2 + 2 * BMQ * 4;
+  static constexpr int LDS_BYTES = 2 * STAGE_BYTES;
+  static constexpr int NSTEP = D / 16;
+  static constexpr int NPV = BMQ / 16;
+  static constexpr int NDB = D / 32;
+};
+
+template <typename Tag, int D, int MODE>
+__global__ __launch_bounds__(256) void dkdv16_kernel(fa_bwd_params p, int num_n_blocks) {
+  using C = Dkdv16Cfg<D>;
+  using EL = Elem<Tag>;
+  using S = uint16_t;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const fa_fwd_params& f = p.fwd;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31;
+  const int bhk_count = f.batch * f.heads_kv;
+  // Low key blocks first: under causal masking they see the most query rows.
+  const int nblk = blockIdx.x / bhk_count;
+  const int bhk = blockIdx.x - nblk * bhk_count;
+  const int b = bhk / f.heads_kv, hk = bhk - b * f.heads_kv;
+  const int group = f.heads_q / f.heads_kv;
+
+  int q_start = 0, sq = f.seqlen_q, k_start = 0, sk = f.seqlen_k;
+  if (f.cu_seqlens_q) {
+    bounded_seq(f.cu_seqlens_q, b, f.total_q, q_start, sq);
+    bounded_seq(f.cu_seqlens_k, b, f.total_k, k_start, sk);
+  }
+  const int n0 = nblk * C::BN;
+  if (n0 >= sk || num_n_blocks <= 0) return;
+
+  const S* kbase = reinterpret_cast<const S*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1] +
+                   (int64_t)k_start * f.k_stride[2];
+  const S* vbase = reinterpret_cast<const S*>(f.v) + b * f.v_stride[0] + hk * f.v_stride[1] +
+                   (int64_t)k_start * f.v_stride[2];
+  const int n0w = n0 + 32 * wave;
+  const int ncols = min(32, sk - n0w);
+  const int n = n0w + l32;
+  const bool nvalid = n < sk;
+  s16x8 kop[C::NSTEP], vop[C::NSTEP];
+  {
+    const S* kr = kbase + (int64_t)(nvalid ? n : 0) * f.k_stride[2] + 8 * h;
+    const S* vr = vbase + (int64_t)(nvalid ? n : 0) * f.v_stride[2] + 8 * h;
+#pragma unroll
+    for (int s = 0; s < C::NSTEP; ++s) {
+      kop[s] = load_op<Tag>(kr + 16 * s);
+      vop[s] = load_op<Tag>(vr + 16 * s);
+    }
+    if (!nvalid) {
+#pragma unroll
+      for (int s = 0; s < C::NSTEP; ++s) { kop[s] = zero_op<Tag>(); vop[s] = zero_op<Tag>(); }
+    }
+    wait_vm_all();
+  }
+
+  f32x16 dk[C::NDB], dv[C::NDB];
+#pragma unroll
+  for (int i = 0; i < C::NDB; ++i) { dk[i] = zero16(); dv[i] = zero16(); }
+
+  SwzTile<C::BMQ, D, C::NT> qt, gt;
+  const int nlast = min(n0 + C::BN, sk) - 1;
+
+  for (int g = 0; g < group; ++g) {
+    const int hq = hk * group + g;
+    const Mods md = make_mods(f, b, hq, sq, sk);
+    const float c = md.scale_log2;
+    const S* qbase = reinterpret_cast<const S*>(f.q) + b * f.q_stride[0] + hq * f.q_stride[1] +
+                     (int64_t)q_start * f.q_stride[2];
+    const S* gbase = reinterpret_cast<const S*>(p.dout) + b * p.dout_stride[0] + hq * p.dout_stride[1] +
+                     (int64_t)q_start * p.dout_stride[2];
+    const float* lbase = f.lse + b * f.lse_stride[0] + hq * f.lse_stride[1] + (int64_t)q_start * f.lse_stride[2];
+    const float* dbase = p.delta + b * p.delta_stride[0] + hq * p.delta_stride[1] +
+                         (int64_t)q_start * p.delta_stride[2];
+    const int64_t qs = f.q_stride[2], gs = p.dout_stride[2];
+
+    int mlo = 0, mhi = sq;
+    if (f.causal) mlo = max(mlo, n0 - md.off);
+    if (f.window_right >= 0) mlo = max(mlo, n0 - md.off - f.window_right);
+    if (f.window_left >= 0) mhi = min(mhi, nlast - md.off + f.window_left + 1);
+    mlo = max(mlo, 0) / C::BMQ * C::BMQ;
+    const int nsteps = mhi > mlo ? (mhi - mlo + C::BMQ - 1) / C::BMQ : 0;
+
+    float lreg = 0.f, dreg = 0.f;  // this thread's lse2 / delta for the next stage
+    auto load_stage = [&](int m0) {
+      qt.load([&](int r) -> const S* { int m = m0 + r; return m < sq ? qbase + (int64_t)m * qs : nullptr; }, qbase, tid);
+      gt.load([&](int r) -> const S* { int m = m0 + r; return m < sq ? gbase + (int64_t)m * gs : nullptr; }, gbase, tid);
+      if (tid < C::BMQ) {
+        const int m = min(m0 + tid, sq - 1);
+        lreg = lbase[(int64_t)m * f.lse_stride[2]];
+        dreg = dbase[(int64_t)m * p.delta_stride[2]];
+      }
+    };
+    auto store_stage = [&](int st, int m0) {
+      unsigned char* base = smem_raw + st * C::STAGE_BYTES;
+      S* sp = reinterpret_cast<S*>(base);
+      qt.store(sp, tid);
+      gt.store(sp + C::QT, tid);
+      if (tid < C::BMQ) {
+        float* lf = reinterpret_cast<float*>(base + 2 * C::QT * 2);
+        lf[tid] = (m0 + tid < sq) ? lse2_of(lreg) : __builtin_inff();
+        lf[C::BMQ + tid] = dreg;
+      }
+    };
+
+    if (nsteps > 0) {
+      load_stage(mlo);
+      store_stage(0, mlo);
+    }
+    __syncthreads();
+    for (int t = 0; t < nsteps; ++t) {
+      const int m0 = mlo + t * C::BMQ;
+      const int st = t & 1;
+      if (t + 1 < nsteps) load_stage(m0 + C::BMQ);
+
+      const int vis = ncols > 0 ? rect_visibility(md, m0, min(C::BMQ, sq - m0), n0w, ncols) : 0;
+      if (vis) {
+        const unsigned char* base = smem_raw + st * C::STAGE_BYTES;
+        const S* Qs = reinterpret_cast<const S*>(base);
+        const S* Gs = Qs + C::QT;
+        const float* L2 = reinterpret_cast<const float*>(base + 2 * C::QT * 2);
+        const float* DL = L2 + C::BMQ;
+
+        f32x16 sacc = zero16(), pacc = zero16();
+#pragma unroll
+        for (int s = 0; s < C::NSTEP; ++s) {
+          sacc = EL::mma(swz_op<D>(Qs, l32, 2 * s + h), kop[s], sacc);
+          pacc = EL::mma(swz_op<D>(Gs, l32, 2 * s + h), vop[s], pacc);
+        }
+        float l2[16], dl[16];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(L2 + 8 * q4 + 4 * h);
+          const f32x4 d = *reinterpret_cast<const f32x4*>(DL + 8 * q4 + 4 * h);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) { l2[4 * q4 + r] = a[r]; dl[4 * q4 + r] = d[r]; }
+        }
+        const bool plain = (MODE == 0) && vis == 2;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float pv, tc = 0.f;
+          if (plain) {
+            pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], c, -l2[i]));
+          } else {
+            const int m = m0 + acc_row(i, h);
+            const float x = score<(MODE >= 1)>(md, sacc[i], m, n, tc);
+            pv = __builtin_amdgcn_exp2f(x - l2[i]);
+            if (vis == 1 && !keep_pos(md, m, n)) pv = 0.f;
+          }
+          float dp = pacc[i], pd = pv;
+          if constexpr (MODE == 2) {
+            if (md.drop_p > 0.f) {
+              const bool keep = dropout_keep(md, m0 + acc_row(i, h), n);
+              pd = keep ? pv * md.drop_scale : 0.f;
+              dp = keep ? dp * md.drop_scale : 0.f;
+            }
+          }
+          float ds = pv * (dp - dl[i]);
+          if constexpr (MODE >= 1) {
+            if (md.cap2 > 0.f) ds *= (1.f - tc * tc);
+          }
+          sacc[i] = pd;
+          pacc[i] = ds;
+        }
+        s16x8 pb[C::NPV], sb[C::NPV];
+#pragma unroll
+        for (int j = 0; j < C::NPV; ++j) {
+          pb[j] = pack_op<Tag>(sacc, j);
+          sb[j] = pack_op<Tag>(pacc, j);
+        }
+#pragma unroll
+        for (int j = 0; j < C::NPV; ++j)
+#pragma unroll
+          for (int db = 0; db < C::NDB; ++db) {
+            dv[db] = EL::mma(tr_op_rowmap<D>(Gs, 0, 32 * db, j, lane), pb[j], dv[db]);
+            dk[db] = EL::mma(tr_op_rowmap<D>(Qs, 0, 32 * db, j, lane), sb[j], dk[db]);
+          }
+      }
+      if (t + 1 < nsteps) store_stage(st ^ 1, m0 + C::BMQ);
+      __syncthreads();
+    }
+  }
+
+  if (!nvalid) return;
+  S* dkr = reinterpret_cast<S*>(p.dk) + b * p.dk_stride[0] + hk * p.dk_stride[1] +
+           (int64_t)(k_start + n) * p.dk_stride[2];
+  S* dvr = reinterpret_cast<S*>(p.dv) + b * p.dv_stride[0] + hk * p.dv_stride[1] +
+           (int64_t)(k_start + n) * p.dv_stride[2];
+  const float sc = f.softmax_scale;
+#pragma unroll
+  for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int d = db * 32 + 8 * gq + 4 * h;
+      s16x4 wk, wv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        wk[r] = (short)EL::from_f(dk[db][4 * gq + r] * sc);
+        wv[r] = (short)EL::from_f(dv[db][4 * gq + r]);
+      }
+      *reinterpret_cast<s16x4*>(dkr + d) = wk;
+      *reinterpret_cast<s16x4*>(dvr + d) = wv;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dQ: each wave owns 32 queries (lane axis of S^T = K Q^T).
+// ---------------------------------------------------------------------------
+template <int D>
+struct Dq16Cfg {
+  static constexpr int NW = 4;
+  static constexpr int NT = 64 * NW;
+  static constexpr int BM = 32 * NW;
+  static constexpr int BN = (D <= 64) ? 64 : 32;
+  static constexpr int KT = BN * D;
+  static constexpr int STAGE = 2 * KT;  // K, V
+  static constexpr int LDS_BYTES = 2 * STAGE * 2;
+  static constexpr int NSTEP = D / 16;
+  static constexpr int NKB = BN / 32;
+  static constexpr int NPV = BN / 16;
+  static constexpr int NDB = D / 32;
+};
+
+template <typename Tag, int D, int MODE>
+__global__ __launch_bounds__(256) void dq16_kernel(fa_bwd_params p, int num_m_blocks) {
+  using C = Dq16Cfg<D>;
+  using EL = Elem<Tag>;
+  using S = uint16_t;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  S* smem = reinterpret_cast<S*>(smem_raw);
+  const fa_fwd_params& f = p.fwd;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31;
+  const int bh_count = f.batch * f.heads_q;
+  const int mb_rev = blockIdx.x / bh_count;
+  const int bh = blockIdx.x - mb_rev * bh_count;
+  const int b = bh / f.heads_q, hq = bh - b * f.heads_q;
+  const int hk = hq / (f.heads_q / f.heads_kv);
+  const int mblk = num_m_blocks - 1 - mb_rev;
+
+  int q_start = 0, sq = f.seqlen_q, k_start = 0, sk = f.seqlen_k;
+  if (f.cu_seqlens_q) {
+    bounded_seq(f.cu_seqlens_q, b, f.total_q, q_start, sq);
+    bounded_seq(f.cu_seqlens_k, b, f.total_k, k_start, sk);
+  }
+  const int m0 = mblk * C::BM;
+  if (m0 >= sq) return;
+
+  const S* kbase = reinterpret_cast<const S*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1] +
+                   (int64_t)k_start * f.k_stride[2];
+  const S* vbase = reinterpret_cast<const S*>(f.v) + b * f.v_stride[0] + hk * f.v_stride[1] +
+                   (int64_t)k_start * f.v_stride[2];
+  const int64_t ks = f.k_stride[2], vs = f.v_stride[2];
+  const Mods md = make_mods(f, b, hq, sq, sk);
+  const float c = md.scale_log2;
+
+  const int mlast = min(m0 + C::BM, sq) - 1;
+  int lo = 0, hi = sk;
+  if (f.causal) hi = min(hi, mlast + md.off + 1);
+  if (f.window_right >= 0) hi = min(hi, mlast + md.off + f.window_right + 1);
+  if (f.window_left >= 0) lo = max(0, m0 + md.off - f.window_left);
+  lo = lo / C::BN * C::BN;
+  const int ntiles = hi > lo ? (hi - lo + C::BN - 1) / C::BN : 0;
+
+  const int m0w = m0 + 32 * wave;
+  const int mrows = min(32, sq - m0w);
+  const int m = m0w + l32;
+  const bool mvalid = m < sq;
+  s16x8 qop[C::NSTEP], gop[C::NSTEP];
+  float lse2 = __builtin_inff(), dlt = 0.f;
+  {
+    const int mm = mvalid ? m : 0;
+    const S* qr = reinterpret_cast<const S*>(f.q) + b * f.q_stride[0] + hq * f.q_stride[1] +
+                  (int64_t)(q_start + mm) * f.q_stride[2] + 8 * h;
+    const S* gr = reinterpret_cast<const S*>(p.dout) + b * p.dout_stride[0] + hq * p.dout_stride[1] +
+                  (int64_t)(q_start + mm) * p.dout_stride[2] + 8 * h;
+#pragma unroll
+    for (int s = 0; s < C::NSTEP; ++s) {
+      qop[s] = load_op<Tag>(qr + 16 * s);
+      gop[s] = load_op<Tag>(gr + 16 * s);
+    }
+    const float l = f.lse[b * f.lse_stride[0] + hq * f.lse_stride[1] + (int64_t)(q_start + mm) * f.lse_stride[2]];
+    const float d = p.delta[b * p.delta_stride[0] + hq * p.delta_stride[1] + (int64_t)(q_start + mm) * p.delta_stride[2]];
+    wait_vm_all();
+    if (mvalid) {
+      lse2 = lse2_of(l);
+      dlt = d;
+    } else {
+#pragma unroll
+      for (int s = 0; s < C::NSTEP; ++s) { qop[s] = zero_op<Tag>(); gop[s] = zero_op<Tag>(); }
+    }
+  }
+
+  f32x16 dq[C::NDB];
+#pragma unroll
+  for (int i = 0; i < C::NDB; ++i) dq[i] = zero16();
+
+  SwzTile<C::BN, D, C::NT> kt, vt;
+  auto load_stage = [&](int n0) {
+    kt.load([&](int r) -> const S* { int nn = n0 + r; return nn < sk ? kbase + (int64_t)nn * ks : nullptr; }, kbase, tid);
+    vt.load([&](int r) -> const S* { int nn = n0 + r; return nn < sk ? vbase + (int64_t)nn * vs : nullptr; }, vbase, tid);
+  };
+  auto store_stage = [&](int st) {
+    S* base = smem + st * C::STAGE;
+    kt.store(base, tid);
+    vt.store(base + C::KT, tid);
+  };
+
+  if (ntiles > 0) {
+    load_stage(lo);
+    store_stage(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int n0 = lo + t * C::BN;
+    const int st = t & 1;
+    if (t + 1 < ntiles) load_stage(n0 + C::BN);
+    const int vis = mrows > 0 ? rect_visibility(md, m0w, mrows, n0, C::BN) : 0;
+    if (vis) {
+      const S* Ks = smem + st * C::STAGE;
+      const S* Vs = Ks + C::KT;
+      f32x16 sacc[C::NKB], pacc[C::NKB];
+#pragma unroll
+      for (int kb2 = 0; kb2 < C::NKB; ++kb2) { sacc[kb2] = zero16(); pacc[kb2] = zero16(); }
+#pragma unroll
+      for (int s = 0; s < C::NSTEP; ++s)
+#pragma unroll
+        for (int kb2 = 0; kb2 < C::NKB; ++kb2) {
+          sacc[kb2] = EL::mma(swz_op<D>(Ks, kb2 * 32 + l32, 2 * s + h), qop[s], sacc[kb2]);
+          pacc[kb2] = EL::mma(swz_op<D>(Vs, kb2 * 32 + l32, 2 * s + h), gop[s], pacc[kb2]);
+        }
+      const bool plain = (MODE == 0) && vis == 2;
+#pragma unroll
+      for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float pv, tc = 0.f;
+          const int nn = n0 + kb2 * 32 + acc_row(i, h);
+          if (plain) {
+            pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb2][i], c, -lse2));
+          } else {
+            const float x = score<(MODE >= 1)>(md, sacc[kb2][i], m, nn, tc);
+            pv = __builtin_amdgcn_exp2f(x - lse2);
+            if (vis == 1 && !keep_pos(md, m, nn)) pv = 0.f;
+          }
+          float dp = pacc[kb2][i];
+          if constexpr (MODE == 2) {
+            if (md.drop_p > 0.f) dp = dropout_keep(md, m, nn) ? dp * md.drop_scale : 0.f;
+          }
+          float ds = pv * (dp - dlt);
+          if constexpr (MODE >= 1) {
+            if (md.cap2 > 0.f) ds *= (1.f - tc * tc);
+          }
+          sacc[kb2][i] = ds;
+        }
+      s16x8 sb[C::NPV];
+#pragma unroll
+      for (int j = 0; j < C::NPV; ++j) sb[j] = pack_op<Tag>(sacc[j >> 1], j & 1);
+#pragma unroll
+      for (int j = 0; j < C::NPV; ++j)
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) dq[db] = EL::mma(tr_op_rowmap<D>(Ks, 0, 32 * db, j, lane), sb[j], dq[db]);
+    }
+    if (t + 1 < ntiles) store_stage(st ^ 1);
+    __syncthreads();
+  }
+
+  if (!mvalid) return;
+  S* dqr = reinterpret_cast<S*>(p.dq) + b * p.dq_stride[0] + hq * p.dq_stride[1] +
+           (int64_t)(q_start + m) * p.dq_stride[2];
+  const float sc = f.softmax_scale;
+#pragma unroll
+  for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      s16x4 w;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[r] = (short)EL::from_f(dq[db][4 * gq + r] * sc);
+      *reinterpret_cast<s16x4*>(dqr + db * 32 + 8 * gq + 4 * h) = w;
+    }
+}
+
+}  // namespace fa

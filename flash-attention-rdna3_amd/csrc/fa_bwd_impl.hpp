@@ -1,4 +1,5 @@
 #pragma once
+#include <type_traits>
 // Kernel templates of fa_bwd; instantiated per dtype by fa_bwd_<dtype>.hip.
 // fa_bwd.hip - FlashAttention-2 backward for gfx950: delta, dK/dV, dQ.
 //
@@ -25,6 +26,7 @@
 //    Q and dO are register B operands, dS^T feeds dQ^T += K^T dS^T directly.
 #include "fa_internal.hpp"
 #include "fa_tiles.hpp"
+#include "fa_bwd16.hpp"
 
 namespace fa {
 
@@ -560,6 +562,32 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
     hipLaunchKernelGGL((bwd_delta_kernel<Tag, D>), grid, dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+  }
+  constexpr bool FAST = !std::is_same<Tag, f32_t>::value && D <= 128;
+  if constexpr (FAST) {
+    if (phases & 2) {
+      using C = Dkdv16Cfg<D>;
+      auto kern = dkdv16_kernel<Tag, D, MODE>;
+      hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
+      if (e != hipSuccess) return e;
+      const int nnb = (f.seqlen_k + C::BN - 1) / C::BN;
+      const long grid = (long)nnb * f.batch * f.heads_kv;
+      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nnb);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    if (phases & 4) {
+      using C = Dq16Cfg<D>;
+      auto kern = dq16_kernel<Tag, D, MODE>;
+      hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
+      if (e != hipSuccess) return e;
+      const int nmb = (f.seqlen_q + C::BM - 1) / C::BM;
+      const long grid = (long)nmb * f.batch * f.heads_q;
+      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
   }
   if (phases & 2) {
     using C = DkdvCfg<Tag, D>;

@@ -1,0 +1,261 @@
+// fa_fwd16.hpp - forward kernel specialised for 16-bit inputs and D <= 128.
+//
+// Same algorithm and results as fwd_kernel (exp2 online softmax,
+// LSE = m*ln2 + ln l; reference kernels/forward.py:28-164 and
+// _common.py:233-345), organised for throughput on gfx950:
+//  * K and V tiles sit row-major in LDS with an XOR chunk swizzle (no
+//    padding, conflict-free reads); S^T = K Q^T reads K with ds_read_b128 and
+//    O^T += V^T P^T reads V^T straight from the row-major tile with
+//    ds_read_b64_tr_b16, so nothing is transposed through registers;
+//  * tiles strictly inside the visible region take an unmasked path whose
+//    per-score work is one FMA + one exp2 + max/sum;
+//  * the running max is updated lazily: P = exp2(s*c - m) is accepted while
+//    the tile max stays within 2^8 of m, and O, l are rescaled (wave-wide)
+//    only when some row's max grows past that, so the O^T rescale leaves the
+//    steady-state loop.  The result is identical up to rounding: O and l are
+//    both expressed relative to the same m, and the final O / l and
+//    lse = (m + log2 l) * ln2 do not depend on which m was used.
+#pragma once
+
+#include <type_traits>
+
+#include "fa_internal.hpp"
+#include "fa_tiles.hpp"
+
+namespace fa {
+
+template <int D>
+struct Fwd16Cfg {
+  static constexpr int NW = 4;
+  static constexpr int NT = 64 * NW;
+  static constexpr int BM = 32 * NW;
+  static constexpr int BN = 64;
+  static constexpr int KTILE = BN * D;  // elements (K), then V
+  static constexpr int STAGE = 2 * KTILE;
+  static constexpr int LDS_BYTES = 2 * STAGE * 2;
+  static constexpr int NSTEP = D / 16;
+  static constexpr int NKB = BN / 32;
+  static constexpr int NPV = BN / 16;
+  static constexpr int NDB = D / 32;
+};
+
+// Largest growth of the running max (log2 domain) absorbed without rescaling.
+constexpr float kLazyRescale = 8.0f;
+
+template <typename Tag, int D, int MODE>
+__global__ __launch_bounds__(256, 2) void fwd16_kernel(fa_fwd_params p, int num_m_blocks) {
+  using C = Fwd16Cfg<D>;
+  using EL = Elem<Tag>;
+  using S = uint16_t;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  S* smem = reinterpret_cast<S*>(smem_raw);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31;
+
+  const int bh_count = p.batch * p.heads_q;
+  const int mb_rev = blockIdx.x / bh_count;
+  const int bh = blockIdx.x - mb_rev * bh_count;
+  const int b = bh / p.heads_q, hq = bh - b * p.heads_q;
+  const int hk = hq / (p.heads_q / p.heads_kv);
+  const int mblk = num_m_blocks - 1 - mb_rev;
+
+  int q_start = 0, sq = p.seqlen_q, k_start = 0, sk = p.seqlen_k;
+  if (p.cu_seqlens_q) {
+    bounded_seq(p.cu_seqlens_q, b, p.total_q, q_start, sq);
+    bounded_seq(p.cu_seqlens_k, b, p.total_k, k_start, sk);
+  }
+  const int m0 = mblk * C::BM;
+  if (m0 >= sq) return;
+
+  const S* qb = reinterpret_cast<const S*>(p.q) + b * p.q_stride[0] + hq * p.q_stride[1] +
+                (int64_t)q_start * p.q_stride[2];
+  const S* kb = reinterpret_cast<const S*>(p.k) + b * p.k_stride[0] + hk * p.k_stride[1] +
+                (int64_t)k_start * p.k_stride[2];
+  const S* vb = reinterpret_cast<const S*>(p.v) + b * p.v_stride[0] + hk * p.v_stride[1] +
+                (int64_t)k_start * p.v_stride[2];
+  const int64_t qs = p.q_stride[2], ks = p.k_stride[2], vs = p.v_stride[2];
+  const Mods md = make_mods(p, b, hq, sq, sk);
+  const float c = md.scale_log2;
+
+  const int mlast = min(m0 + C::BM, sq) - 1;
+  int lo = 0, hi = sk;
+  if (p.causal) hi = min(hi, mlast + md.off + 1);
+  if (p.window_right >= 0) hi = min(hi, mlast + md.off + p.window_right + 1);
+  if (p.window_left >= 0) lo = max(0, m0 + md.off - p.window_left);
+  lo = lo / C::BN * C::BN;
+  const int ntiles = hi > lo ? (hi - lo + C::BN - 1) / C::BN : 0;
+
+  const int m0w = m0 + 32 * wave;
+  const int mrows = min(32, sq - m0w);
+  const int m = m0w + l32;
+  const bool mvalid = m < sq;
+
+  s16x8 qop[C::NSTEP];
+  {
+    const S* qrow = qb + (int64_t)(mvalid ? m : 0) * qs + 8 * h;
+#pragma unroll
+    for (int s = 0; s < C::NSTEP; ++s) qop[s] = load_op<Tag>(qrow + 16 * s);
+    if (!mvalid) {
+#pragma unroll
+      for (int s = 0; s < C::NSTEP; ++s) qop[s] = zero_op<Tag>();
+    }
+    wait_vm_all();
+  }
+
+  float m_i = kNegInf, l_i = 0.f;
+  f32x16 acc[C::NDB];
+#pragma unroll
+  for (int i = 0; i < C::NDB; ++i) acc[i] = zero16();
+
+  SwzTile<C::BN, D, C::NT> kt, vt;
+  auto load_tiles = [&](int n0) {
+    kt.load([&](int r) -> const S* { int n = n0 + r; return n < sk ? kb + (int64_t)n * ks : nullptr; }, kb, tid);
+    vt.load([&](int r) -> const S* { int n = n0 + r; return n < sk ? vb + (int64_t)n * vs : nullptr; }, vb, tid);
+  };
+  auto store_tiles = [&](int stage) {
+    S* base = smem + stage * C::STAGE;
+    kt.store(base, tid);
+    vt.store(base + C::KTILE, tid);
+  };
+
+  if (ntiles > 0) {
+    load_tiles(lo);
+    store_tiles(0);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int n0 = lo + t * C::BN;
+    const int stage = t & 1;
+    if (t + 1 < ntiles) load_tiles(n0 + C::BN);
+
+    const int vis = mrows > 0 ? rect_visibility(md, m0w, mrows, n0, C::BN) : 0;
+    if (vis) {
+      const S* Ks = smem + stage * C::STAGE;
+      const S* Vs = Ks + C::KTILE;
+      f32x16 sacc[C::NKB];
+#pragma unroll
+      for (int kb2 = 0; kb2 < C::NKB; ++kb2) sacc[kb2] = zero16();
+#pragma unroll
+      for (int s = 0; s < C::NSTEP; ++s)
+#pragma unroll
+        for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+          sacc[kb2] = EL::mma(swz_op<D>(Ks, kb2 * 32 + l32, 2 * s + h), qop[s], sacc[kb2]);
+
+      // Scores -> log2 domain (masked or modified when needed), tile max.
+      float tmax = kNegInf;
+      const bool plain = (MODE == 0) && vis == 2 && c > 0.f;
+      if (plain) {
+#pragma unroll
+        for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sacc[kb2][i]);
+        tmax *= c;  // the plain path is only taken for c > 0
+      } else {
+#pragma unroll
+        for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int n = n0 + kb2 * 32 + acc_row(i, h);
+            float tc;
+            float x = score<(MODE >= 1)>(md, sacc[kb2][i], m, n, tc);
+            if (vis == 1 && !keep_pos(md, m, n)) x = kNegInf;
+            sacc[kb2][i] = x;
+            tmax = fmaxf(tmax, x);
+          }
+      }
+      tmax = fmaxf(tmax, xor32(tmax));
+      // Lazy rescale, decided for the whole wave.
+      if (__builtin_amdgcn_ballot_w64(tmax > m_i + kLazyRescale)) {
+        const float m_new = fmaxf(m_i, tmax);
+        const float alpha = (m_new == kNegInf) ? 1.f : __builtin_amdgcn_exp2f(m_i - m_new);
+        l_i *= alpha;
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) acc[db] *= alpha;
+        m_i = m_new;
+      }
+      const float m_use = (m_i == kNegInf) ? 0.f : m_i;
+      float rsum = 0.f;
+      if (plain) {
+        const float mc = -m_use;
+#pragma unroll
+        for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb2][i], c, mc));
+            sacc[kb2][i] = pv;
+            rsum += pv;
+          }
+      } else {
+#pragma unroll
+        for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float pv = __builtin_amdgcn_exp2f(sacc[kb2][i] - m_use);
+            sacc[kb2][i] = pv;
+            rsum += pv;
+          }
+      }
+      rsum += xor32(rsum);
+      l_i += rsum;
+      if constexpr (MODE == 2) {
+        if (md.drop_p > 0.f) {
+#pragma unroll
+          for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int n = n0 + kb2 * 32 + acc_row(i, h);
+              sacc[kb2][i] = dropout_keep(md, m, n) ? sacc[kb2][i] * md.drop_scale : 0.f;
+            }
+        }
+      }
+      // O^T += V^T P^T (bf16: P as hi + lo parts, see fwd_kernel).
+      constexpr bool PSPLIT = std::is_same<Tag, bf16_t>::value;
+      s16x8 pb[C::NPV], pl[PSPLIT ? C::NPV : 1];
+#pragma unroll
+      for (int j = 0; j < C::NPV; ++j) pb[j] = pack_op<Tag>(sacc[j >> 1], j & 1);
+      if constexpr (PSPLIT) {
+#pragma unroll
+        for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sacc[kb2][i] -= EL::to_f(EL::from_f(sacc[kb2][i]));
+#pragma unroll
+        for (int j = 0; j < C::NPV; ++j) pl[j] = pack_op<Tag>(sacc[j >> 1], j & 1);
+      }
+#pragma unroll
+      for (int j = 0; j < C::NPV; ++j)
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) {
+          const s16x8 a = tr_op_rowmap<D>(Vs, 0, 32 * db, j, lane);
+          acc[db] = EL::mma(a, pb[j], acc[db]);
+          if constexpr (PSPLIT) acc[db] = EL::mma(a, pl[j], acc[db]);
+        }
+    }
+
+    if (t + 1 < ntiles) store_tiles(stage ^ 1);
+    __syncthreads();
+  }
+
+  if (!mvalid) return;
+  const float l_safe = (l_i == 0.f) ? 1.f : l_i;
+  const float inv = 1.f / l_safe;
+  S* orow = reinterpret_cast<S*>(p.out) + b * p.out_stride[0] + hq * p.out_stride[1] +
+            (int64_t)(q_start + m) * p.out_stride[2];
+#pragma unroll
+  for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      s16x4 w;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[r] = (short)EL::from_f(acc[db][4 * g + r] * inv);
+      *reinterpret_cast<s16x4*>(orow + db * 32 + 8 * g + 4 * h) = w;
+    }
+  if (h == 0) {
+    float* lb = p.lse + b * p.lse_stride[0] + hq * p.lse_stride[1] + (int64_t)(q_start + m) * p.lse_stride[2];
+    *lb = (m_i == kNegInf || l_i == 0.f) ? kNegInf : (m_i + __log2f(l_safe)) * kLn2;
+  }
+}
+
+}  // namespace fa

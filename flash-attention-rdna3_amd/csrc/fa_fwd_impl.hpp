@@ -25,6 +25,7 @@
 
 #include "fa_internal.hpp"
 #include "fa_tiles.hpp"
+#include "fa_fwd16.hpp"
 
 namespace fa {
 
@@ -274,6 +275,17 @@ __global__ __launch_bounds__(256) void fwd_kernel(fa_fwd_params p, int num_m_blo
 
 template <typename Tag, int D, int MODE>
 static hipError_t run_fwd(const fa_fwd_params& p, hipStream_t stream) {
+  if constexpr (!std::is_same<Tag, f32_t>::value && D <= 128) {
+    using C = Fwd16Cfg<D>;
+    auto kern = fwd16_kernel<Tag, D, MODE>;
+    hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    const int nmb = (p.seqlen_q + C::BM - 1) / C::BM;
+    const long grid = (long)nmb * p.batch * p.heads_q;
+    if (grid <= 0) return hipSuccess;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb);
+    return hipGetLastError();
+  }
   using C = FwdCfg<Tag, D>;
   auto kern = fwd_kernel<Tag, D, MODE>;
   hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);

@@ -128,3 +128,93 @@ struct TransTile {
 };
 
 }  // namespace fa
+
+namespace fa {
+
+// ---------------------------------------------------------------------------
+// Swizzled row-major LDS tiles for 16-bit data (no padding).
+//
+// A tile row of COLS elements is COLS/8 chunks of 16 bytes; chunk c of row r
+// is stored at chunk slot c ^ swz(r).  swz is chosen per row width so that
+// both read patterns the kernels use are bank-conflict free on the 64-bank
+// LDS:
+//  * ds_read_b128 of one chunk from 16 consecutive rows (MFMA operand with
+//    the contracted index along the row), and
+//  * ds_read_b64_tr_b16 over an aligned block of 4 rows x 4 chunks (MFMA
+//    operand with the contracted index along the column; see tr_op_rowmap).
+// ---------------------------------------------------------------------------
+template <int COLS>
+__device__ constexpr inline int swz(int r) {
+  constexpr int CPR = COLS / 8;
+  if constexpr (CPR >= 16) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else if constexpr (CPR == 8) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else return (r >> 2) & 3;
+}
+
+template <int COLS>
+__device__ constexpr inline int swz_off(int r, int col) {
+  return r * COLS + (((col >> 3) ^ swz<COLS>(r)) << 3) + (col & 7);
+}
+
+template <int R, int COLS, int NT>
+struct SwzTile {
+  static constexpr int CPR = COLS / 8;
+  static constexpr int CH = R * CPR;
+  static constexpr int PT = (CH + NT - 1) / NT;
+  uint4 r[PT];
+  uint32_t ok;
+
+  template <typename RowPtr>
+  __device__ inline void load(RowPtr rowptr, const uint16_t* fallback, int tid) {
+    ok = 0;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      const int c = tid + NT * j;
+      const uint16_t* p = (CH % NT == 0 || c < CH) ? rowptr(c / CPR) : nullptr;
+      ok |= (p != nullptr ? 1u : 0u) << j;
+      p = p ? p : fallback;
+      r[j] = *reinterpret_cast<const uint4*>(p + (c % CPR) * 8);
+    }
+  }
+  __device__ inline void store(uint16_t* lds, int tid) const {
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      const int c = tid + NT * j;
+      if (CH % NT == 0 || c < CH) {
+        const int row = c / CPR, ch = c % CPR;
+        *reinterpret_cast<uint4*>(lds + row * COLS + ((ch ^ swz<COLS>(row)) << 3)) = masked(r[j], (ok >> j) & 1u);
+      }
+    }
+  }
+};
+
+// B/A operand (8 x 16-bit) of row `row`, k-chunk `chunk` of a swizzled tile.
+template <int COLS>
+__device__ inline s16x8 swz_op(const uint16_t* tile, int row, int chunk) {
+  return *reinterpret_cast<const s16x8*>(tile + row * COLS + ((chunk ^ swz<COLS>(row)) << 3));
+}
+
+// A operand for a product contracting over the TILE ROW index whose k-slots
+// follow a 32x32 accumulator's row map (the layout pack_op produces): slot e
+// of lane half h is tile row rbase + 32*(j/2) + 16*(j%2) + 8*(e/4) + 4h + e%4,
+// operand row (lane%32) is tile column cbase + lane%32.  Two
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4
+// of the 4-element chunks read by lanes 4e + i/4, so lane `src` of a group
+// reads 4 columns at row (src/4) of the 4-row block and the result is the
+// column of the block.
+template <int COLS>
+__device__ inline s16x8 tr_op_rowmap(const uint16_t* tile, int rbase, int cbase, int j, int lane) {
+  const int h = lane >> 5;
+  const int row0 = rbase + 32 * (j >> 1) + 16 * (j & 1) + 4 * h + ((lane & 15) >> 2);
+  const int col = cbase + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s4 lds_s4;
+  const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s4*)(const_cast<uint16_t*>(tile) + swz_off<COLS>(row0, col)));
+  const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s4*)(const_cast<uint16_t*>(tile) + swz_off<COLS>(row0 + 8, col)));
+  s16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return r;
+}
+
+}  // namespace fa
