@@ -53,6 +53,12 @@ struct DecodeArgs {
   float* ws_lse;        // [splits][B][Hq][Sq] fp32
 };
 
+}  // namespace fa
+
+#include "fa_decode2.hpp"
+
+namespace fa {
+
 template <typename Tag, int D>
 struct DecCfg {
   using EL = Elem<Tag>;
@@ -303,6 +309,25 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
 
 template <typename Tag, int D, bool PAGED>
 static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
+  // Paged caches with blocks under 16 keys take the generic kernel (their
+  // per-row page lookups would enter the streaming kernel's vmcnt sequence).
+  if constexpr (D <= 128) {
+    if (!PAGED || a.block_shift >= 4) {
+      using C = Dec2Cfg<D>;
+      const int group = a.heads_q / a.heads_kv;
+      const int nrb = (group * a.seqlen_q + 15) / 16;
+      dim3 grid(a.num_splits, a.batch * a.heads_kv * nrb);
+      auto kern = decode2_kernel<Tag, D, PAGED ? 1 : 0>;
+      hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(kern, grid, dim3(C::NT), C::LDS_BYTES, stream, a);
+      e = hipGetLastError();
+      if (e != hipSuccess || a.num_splits == 1) return e;
+      const int rows = a.batch * a.heads_q * a.seqlen_q;
+      hipLaunchKernelGGL((decode_combine2_kernel<Tag, D>), dim3((rows + 3) / 4), dim3(256), 0, stream, a);
+      return hipGetLastError();
+    }
+  }
   using C = DecCfg<Tag, D>;
   auto kern = decode_kernel<Tag, D, PAGED>;
   hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);

@@ -1,0 +1,402 @@
+// fa_decode2.hpp - streaming decode kernel (16-bit, D <= 128), contiguous or
+// paged cache.  Same results as decode_kernel (reference kernels/decode.py:9-125,
+// kernels/paged.py:16-89); organised for HBM throughput on gfx950:
+//
+//  * K rows load straight into registers in the MFMA operand layout; V bytes
+//    go HBM -> LDS with global_load_lds_dwordx4 (each lane picks the source
+//    of its 16-byte LDS slot, which both gathers paged rows and applies the
+//    XOR swizzle of the LDS tile).
+//  * Every wave streams its own 32-key chunks through NBUF private slots
+//    (up to 64 KB in flight per wave) and synchronises only with itself
+//    (s_waitcnt), so the workgroup never stalls on a barrier in the key loop.
+//  * Scores use v_mfma_f32_16x16x32: the packed GQA rows (group heads x Sq,
+//    usually 4) occupy 16 MFMA columns instead of 32.  P^T feeds the P.V MFMA
+//    from its accumulator; V^T comes from the row-major LDS tile through
+//    ds_read_b64_tr_b16.
+//  * The 4 wave states are merged in LDS, so one partial per workgroup (or
+//    the final row, with a single split) reaches HBM.
+#pragma once
+
+#include "fa_internal.hpp"
+#include "fa_tiles.hpp"
+
+namespace fa {
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+template <typename Tag> __device__ inline f32x4v mma16(s16x8 a, s16x8 b, f32x4v c);
+template <> __device__ inline f32x4v mma16<f16_t>(s16x8 a, s16x8 b, f32x4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h16x8, a), __builtin_bit_cast(h16x8, b), c, 0, 0, 0);
+}
+template <> __device__ inline f32x4v mma16<bf16_t>(s16x8 a, s16x8 b, f32x4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b16x8, a), __builtin_bit_cast(b16x8, b), c, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+template <int D>
+struct Dec2Cfg {
+  static constexpr int NW = 4;
+  static constexpr int NT = 64 * NW;
+  static constexpr int CK = 32;                      // keys per chunk
+  static constexpr int CPR = D / 8;                  // 16-byte chunks per row
+  static constexpr int TILE = CK * D;                // elements of a V tile
+  static constexpr int NSTEP = D / 32;               // 16x16x32 k-steps
+  static constexpr int NDB = D / 16;                 // 16-wide blocks of O^T
+  static constexpr int KLOADS = 2 * NSTEP;           // K dwordx4 loads per chunk per lane
+  static constexpr int VLOADS = CK * CPR / 64;       // V dwordx4 loads per chunk per lane
+  static constexpr int PER = KLOADS + VLOADS;        // vector-memory ops per chunk
+  // Chunk slots per wave (each slot is 4*PER VGPRs per lane).
+#ifndef FA_DEC_SLOT_VGPRS
+#define FA_DEC_SLOT_VGPRS 128
+#endif
+  static constexpr int NBUF = FA_DEC_SLOT_VGPRS / (4 * PER);
+  static constexpr int WAVE_ELEMS = TILE;            // one private V tile per wave
+  static constexpr int LOOP_BYTES = NW * WAVE_ELEMS * 2;
+  static constexpr int OLD = 17;                     // merge buffer row stride (floats)
+  static constexpr int MERGE_BYTES = NW * D * OLD * 4 + 2 * NW * 16 * 4;
+  static constexpr int LDS_BYTES = LOOP_BYTES > MERGE_BYTES ? LOOP_BYTES : MERGE_BYTES;
+};
+
+// PAGE: 0 contiguous cache; 1 paged with block_size >= 16 (a 32-key chunk
+// spans at most two pages, whose ids are wave-uniform scalar loads).
+//
+// Pipeline: each wave owns NBUF chunk slots of registers.  Slot j holds chunk
+// k = NBUF*i + j: K in the MFMA A layout (lane row l%16, 8 dims per k-step)
+// and V as the raw 16-byte pieces of the chunk's rows.  A chunk's V goes to
+// the wave's private swizzled LDS tile just before use and is read back
+// transposed.  Every slot is refilled right after it is consumed,
+// unconditionally (slots past the wave's last chunk load a readable stand-in
+// row), so NBUF-1 chunks stay in flight while one is computed.  All loads are
+// ordinary vector loads into registers: the compiler's per-register vmcnt
+// tracking then waits exactly for the slot being used.  (Asynchronous LDS DMA
+// in this loop makes it drain every load at the loop head instead.)
+template <typename Tag, int D, int PAGE>
+__global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
+  static_assert(PAGE == 0 || PAGE == 1, "decode2 handles contiguous and >=16-key pages");
+  constexpr bool PAGED = PAGE != 0;
+  using C = Dec2Cfg<D>;
+  using EL = Elem<Tag>;
+  using S = uint16_t;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4, l16 = lane & 15;
+  const int split = blockIdx.x;
+  const int group = a.heads_q / a.heads_kv;
+  const int rows = group * a.seqlen_q;
+  const int nrb = (rows + 15) / 16;
+  const int rb = blockIdx.y % nrb;
+  const int bhk = blockIdx.y / nrb;
+  const int b = bhk / a.heads_kv, hk = bhk - b * a.heads_kv;
+
+  int len = a.max_len;
+  if (a.lens) len = min(max(a.lens[b * a.lens_stride], 0), a.max_len);
+  const int nch = (len + C::CK - 1) / C::CK;
+  const int per = nch / a.num_splits, extra = nch % a.num_splits;
+  const int c0 = split * per + min(split, extra);
+  const int cnt = per + (split < extra ? 1 : 0);
+
+  // This lane's packed query column (group head, query row).
+  const int r = rb * 16 + l16;
+  const bool rvalid = r < rows;
+  const int gq = rvalid ? r / a.seqlen_q : 0;
+  const int mq = rvalid ? r - gq * a.seqlen_q : 0;
+  const int hq = hk * group + gq;
+  s16x8 qop[C::NSTEP];
+  {
+    const S* qrow = reinterpret_cast<const S*>(a.q) + b * a.q_stride[0] + hq * a.q_stride[1] + mq * a.q_stride[2];
+#pragma unroll
+    for (int s = 0; s < C::NSTEP; ++s) qop[s] = load_op<Tag>(qrow + 8 * (4 * s + g4));
+    wait_vm_all();
+    if (!rvalid) {
+#pragma unroll
+      for (int s = 0; s < C::NSTEP; ++s) qop[s] = zero_op<Tag>();
+    }
+  }
+
+  typedef __attribute__((address_space(3))) void lds_void;
+  const S* kbase = reinterpret_cast<const S*>(a.k);
+  const S* vbase = reinterpret_cast<const S*>(a.v);
+  if constexpr (!PAGED) {
+    kbase += b * a.k_stride[0] + hk * a.k_stride[1];
+    vbase += b * a.v_stride[0] + hk * a.v_stride[1];
+  } else {
+    kbase += hk * a.k_stride[2];
+    vbase += hk * a.v_stride[2];
+  }
+  const int bs_mask = (1 << a.block_shift) - 1;
+  S* wbase = reinterpret_cast<S*>(smem_raw) + wave * C::WAVE_ELEMS;
+
+  // Page ids are read through the constant address space so the compiler
+  // issues scalar loads (lgkmcnt): a vector load would enter the vmcnt
+  // sequence the pipeline counts on.
+  typedef const __attribute__((address_space(4))) int32_t const_i32;
+  const_i32* btab = (const_i32*)a.block_table;
+  const int64_t bt_row = (int64_t)b * a.bt_stride[0];
+  // Page ids of the (at most two) pages holding rows [0,16) and [16,32) of a
+  // chunk (uniform across the wave).
+  auto chunk_pages = [&](int c, int& pg0, int& pg1) {
+    const int n0 = c * C::CK;
+    const int last = (a.max_len - 1) >> a.block_shift;
+    pg0 = btab[bt_row + (int64_t)min(n0 >> a.block_shift, last) * a.bt_stride[1]];
+    pg1 = btab[bt_row + (int64_t)min((n0 + 16) >> a.block_shift, last) * a.bt_stride[1]];
+  };
+  // Element offset of key n's row from the per-(b, hk) base, or -1 if absent
+  // (branch-free).
+  auto key_off = [&](int n, int pg0, int pg1, const int64_t* st) -> int64_t {
+    bool ok = n < len;
+    int64_t off;
+    if constexpr (PAGE == 0) {
+      off = (int64_t)n * st[2];
+    } else {
+      const int phys = ((n & 31) < 16) ? pg0 : pg1;
+      ok = ok && phys >= 0 && phys < a.num_blocks;
+      off = (int64_t)phys * st[0] + (int64_t)(n & bs_mask) * st[1];
+    }
+    return ok ? off : -1;
+  };
+
+  // Chunk slot j: K registers kr[j], V registers vr[j].  `live` false loads
+  // the stand-in row 0 (nothing of it is used).
+  s16x8 kr[C::NBUF][2][C::NSTEP];
+  s16x8 vreg[C::NBUF][C::VLOADS];
+  auto issue_chunk = [&](int c, bool live, s16x8 (&kd)[2][C::NSTEP], s16x8 (&vd)[C::VLOADS]) {
+    const int n0 = c * C::CK;
+    int pg0 = 0, pg1 = 0;
+    if constexpr (PAGE == 1) chunk_pages(c, pg0, pg1);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      int64_t ko = key_off(n0 + 16 * kb + l16, pg0, pg1, a.k_stride);
+      ko = (ko < 0 || !live) ? 0 : ko;
+#pragma unroll
+      for (int s = 0; s < C::NSTEP; ++s) kd[kb][s] = load_op<Tag>(kbase + ko + 8 * (4 * s + g4));
+    }
+#pragma unroll
+    for (int i = 0; i < C::VLOADS; ++i) {
+      const int slot = 64 * i + lane;
+      const int row = slot / C::CPR;
+      int64_t vo = key_off(n0 + row, pg0, pg1, a.v_stride);
+      vo = (vo < 0 || !live) ? 0 : vo;
+      vd[i] = *reinterpret_cast<const s16x8*>(vbase + vo + (slot % C::CPR) * 8);
+    }
+  };
+  // Bit k of the result: key n0 + k of the chunk is visible.
+  auto chunk_mask = [&](int c) -> uint32_t {
+    int pg0 = 0, pg1 = 0;
+    if constexpr (PAGE == 1) chunk_pages(c, pg0, pg1);
+    const int n = c * C::CK + (lane & 31);
+    const bool ok = key_off(n, pg0, pg1, a.k_stride) >= 0;
+    return (uint32_t)__builtin_amdgcn_ballot_w64(ok && lane < 32);
+  };
+
+  float m_i = kNegInf, l_i = 0.f;
+  f32x4v acc[C::NDB];
+#pragma unroll
+  for (int i = 0; i < C::NDB; ++i) acc[i] = f32x4v{0.f, 0.f, 0.f, 0.f};
+
+  S* const Vs = wbase;
+  auto compute_chunk = [&](int c, const s16x8 (&kd)[2][C::NSTEP], const s16x8 (&vd)[C::VLOADS]) {
+    const uint32_t vmask = chunk_mask(c);
+    // V rows -> this wave's LDS tile (swizzled); the previous chunk's reads of
+    // the tile precede these writes in the wave's LDS order.
+#pragma unroll
+    for (int i = 0; i < C::VLOADS; ++i) {
+      const int slot = 64 * i + lane;
+      *reinterpret_cast<s16x8*>(Vs + swz_off<D>(slot / C::CPR, (slot % C::CPR) * 8)) = vd[i];
+    }
+    f32x4v sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sacc[kb] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < C::NSTEP; ++s) sacc[kb] = mma16<Tag>(kd[kb][s], qop[s], sacc[kb]);
+    }
+    float tmax = kNegInf;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = 16 * kb + 4 * g4 + i;
+        const float x = ((vmask >> key) & 1u) ? sacc[kb][i] * a.scale_log2 : kNegInf;
+        sacc[kb][i] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_i, tmax);
+    const float m_use = (m_new == kNegInf) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
+    float rsum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pv = __builtin_amdgcn_exp2f(sacc[kb][i] - m_use);
+        sacc[kb][i] = pv;
+        rsum += pv;
+      }
+    rsum += __shfl_xor(rsum, 16, 64);
+    rsum += __shfl_xor(rsum, 32, 64);
+    l_i = l_i * alpha + rsum;
+    m_i = m_new;
+    s16x8 pb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pb[i] = (short)EL::from_f(sacc[0][i]);
+      pb[4 + i] = (short)EL::from_f(sacc[1][i]);
+    }
+    // V^T operand: group g4 holds keys 4*g4 + e and 16 + 4*g4 + e of column
+    // block db (ds_read_b64_tr_b16 lane semantics as in tr_op_rowmap).  Rows
+    // r and r + 16 share the swizzle.
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s4 lds_s4;
+    const int trow = 4 * g4 + ((lane & 15) >> 2);
+    s16x4 vr[2 * C::NDB];
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db) {
+      S* p = const_cast<S*>(Vs) + swz_off<D>(trow, 16 * db + 4 * (lane & 3));
+      const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)p);
+      const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p + 16 * D));
+      vr[2 * db] = s16x4{lo[0], lo[1], lo[2], lo[3]};
+      vr[2 * db + 1] = s16x4{hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db) {
+      const s16x4 lo = vr[2 * db], hi = vr[2 * db + 1];
+      const s16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      acc[db] *= alpha;
+      acc[db] = mma16<Tag>(va, pb, acc[db]);
+    }
+  };
+
+  // Chunks of this wave: c0 + wave + NW*k, k < mine.
+  const int mine = cnt > wave ? (cnt - wave + C::NW - 1) / C::NW : 0;
+  const int groups = (mine + C::NBUF - 1) / C::NBUF;
+#pragma unroll
+  for (int j = 0; j < C::NBUF; ++j) issue_chunk(c0 + wave + C::NW * j, j < mine, kr[j], vreg[j]);
+  // Steady state: every slot is refilled after use.
+  for (int gi = 0; gi + 1 < groups; ++gi) {
+#pragma unroll
+    for (int j = 0; j < C::NBUF; ++j) {
+      const int k = gi * C::NBUF + j;
+      compute_chunk(c0 + wave + C::NW * k, kr[j], vreg[j]);
+      const int kn = k + C::NBUF;
+      issue_chunk(c0 + wave + C::NW * kn, kn < mine, kr[j], vreg[j]);
+    }
+  }
+  // Last group: everything it needs is in flight.
+  if (groups > 0) {
+#pragma unroll
+    for (int j = 0; j < C::NBUF; ++j) {
+      const int k = (groups - 1) * C::NBUF + j;
+      if (k < mine) compute_chunk(c0 + wave + C::NW * k, kr[j], vreg[j]);
+    }
+  }
+
+  // Merge the wave states through LDS.
+  __syncthreads();
+  float* ow = reinterpret_cast<float*>(smem_raw);
+  float* mw = ow + C::NW * D * C::OLD;
+  float* lw = mw + C::NW * 16;
+#pragma unroll
+  for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ow[(wave * D + 16 * db + 4 * g4 + i) * C::OLD + l16] = acc[db][i];
+  if (g4 == 0) {
+    mw[wave * 16 + l16] = m_i;
+    lw[wave * 16 + l16] = l_i;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < 16 * D; idx += C::NT) {
+    const int cc = idx / D, d = idx - (idx / D) * D;
+    const int row = rb * 16 + cc;
+    if (row >= rows) continue;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < C::NW; ++w) M = fmaxf(M, mw[w * 16 + cc]);
+    const float Mu = (M == kNegInf) ? 0.f : M;
+    float L = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < C::NW; ++w) {
+      const float sc = __builtin_amdgcn_exp2f(mw[w * 16 + cc] - Mu);
+      L += lw[w * 16 + cc] * sc;
+      o += ow[(w * D + d) * C::OLD + cc] * sc;
+    }
+    const float Ls = (L == 0.f) ? 1.f : L;
+    o /= Ls;
+    const int gg = row / a.seqlen_q, mm = row - gg * a.seqlen_q;
+    const int hh = hk * group + gg;
+    if (a.num_splits == 1) {
+      S* op = reinterpret_cast<S*>(a.out) + b * a.out_stride[0] + hh * a.out_stride[1] + mm * a.out_stride[2];
+      op[d] = EL::from_f(o);
+    } else {
+      const int64_t prow = (((int64_t)split * a.batch + b) * a.heads_q + hh) * a.seqlen_q + mm;
+      a.ws_o[prow * a.head_dim + d] = o;
+      if (d == 0) a.ws_lse[prow] = (M == kNegInf || L == 0.f) ? kNegInf : (M + __log2f(L)) * kLn2;
+    }
+  }
+}
+
+// One wave per output row: out = sum_s w_s O_s / sum_s w_s with
+// w_s = exp(lse_s - max_s lse_s).  Lane s reads lse_s (splits <= 64), the
+// weights come from a wave reduction, then each lane sums its D/64 dims over
+// all splits with the loads of up to 8 splits in flight at once.
+template <typename Tag, int D>
+__global__ __launch_bounds__(256) void decode_combine2_kernel(DecodeArgs a) {
+  using EL = Elem<Tag>;
+  constexpr int DPL = D / 64 > 0 ? D / 64 : 1;  // dims per lane (lanes >= D idle when D < 64)
+  const int rows = a.batch * a.heads_q * a.seqlen_q;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t plane = rows;
+  const int ns = a.num_splits;
+  const float ls = lane < ns ? a.ws_lse[lane * plane + row] : kNegInf;
+  float M = ls;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  const float Mu = (M == kNegInf) ? 0.f : M;
+  const float w = (ls == kNegInf) ? 0.f : __expf(ls - Mu);
+  float den = w;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+  const int d0 = lane * DPL;
+  const bool active = d0 < D;
+  float num[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) num[e] = 0.f;
+  const float* src = a.ws_o + (int64_t)row * D + (active ? d0 : 0);
+  for (int s0 = 0; s0 < ns; s0 += 8) {
+    float part[8][DPL];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = min(s0 + u, ns - 1);
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) part[u][e] = src[(int64_t)s * plane * D + e];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float ws = __shfl(w, min(s0 + u, 63), 64);
+      const float wu = (s0 + u < ns) ? ws : 0.f;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) num[e] += wu * part[u][e];
+    }
+  }
+  if (!active) return;
+  const float inv = 1.f / (den == 0.f ? 1.f : den);
+  const int mm = row % a.seqlen_q;
+  const int hh = (row / a.seqlen_q) % a.heads_q;
+  const int bb = row / (a.seqlen_q * a.heads_q);
+  uint16_t* op = reinterpret_cast<uint16_t*>(a.out) + bb * a.out_stride[0] + hh * a.out_stride[1] + mm * a.out_stride[2];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) op[d0 + e] = EL::from_f(num[e] * inv);
+}
+
+}  // namespace fa

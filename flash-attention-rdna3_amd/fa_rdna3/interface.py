@@ -83,6 +83,20 @@ def _paged_num_splits(batch, heads, block_size, max_blocks, target_programs,
     return min(split_cap, max(occupancy_splits, work_splits))
 
 
+def _streaming_decode_splits(batch, kv_heads, packed_rows, max_keys, cus):
+    """Split count for the streaming decode kernel (head_dim <= 128).
+
+    That kernel packs the query heads of one KV head into a 16-column block,
+    runs one 4-wave workgroup per CU and keeps each wave's chunk loads in
+    flight, so the best grid is about one workgroup per CU; each split keeps
+    at least 8 chunks of 32 keys (2 per wave) so the partials and their
+    merge stay small next to the K/V stream.
+    """
+    workgroups = batch * kv_heads * _cdiv(packed_rows, 16)
+    chunks = _cdiv(max(max_keys, 1), 32)
+    return max(1, min(32, _cdiv(cus, workgroups), _cdiv(chunks, 8)))
+
+
 def _cu_count(device):
     return torch.cuda.get_device_properties(device).multi_processor_count
 
@@ -464,8 +478,12 @@ def flash_attention_decode(query, key, value, softmax_scale=None, *, cache_seqle
 
     kdim = _kernel_head_dim(head_dim)
     q, k, v = _prep(_pad_head_dim(query, kdim), _pad_head_dim(key, kdim), _pad_head_dim(value, kdim))
-    target_programs = 4 * _cu_count(query.device)
-    num_splits = _decode_num_splits(batch, heads, seqlen_q, seqlen_k, target_programs)
+    if kdim <= 128:
+        group = heads // key.shape[1]
+        num_splits = _streaming_decode_splits(batch, key.shape[1], group * seqlen_q, seqlen_k,
+                                              _cu_count(query.device))
+    else:
+        num_splits = _decode_num_splits(batch, heads, seqlen_q, seqlen_k, 4 * _cu_count(query.device))
     out = torch.empty((batch, heads, seqlen_q, kdim), dtype=query.dtype, device=query.device)
     workspace = torch.empty(
         _native.decode_workspace_bytes(batch, heads, seqlen_q, kdim, num_splits),
@@ -626,10 +644,17 @@ def flash_attention_decode_paged(query, k_cache, v_cache, block_table, context_l
     num_blocks, block_size, kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
     softmax_scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
 
-    target_programs = 2 * _cu_count(query.device)
-    splits = int(_paged_num_splits(batch, q_heads, block_size, block_table.shape[1], target_programs,
-                                   max_context_len=max_context_len, requested_splits=num_splits))
     kdim = _kernel_head_dim(head_dim)
+    if num_splits is None and kdim <= 128 and block_size >= 16:
+        max_keys = block_table.shape[1] * block_size
+        if max_context_len is not None:
+            max_keys = min(max_keys, max_context_len)
+        splits = _streaming_decode_splits(batch, kv_heads, q_heads // kv_heads, max_keys,
+                                          _cu_count(query.device))
+    else:
+        splits = int(_paged_num_splits(batch, q_heads, block_size, block_table.shape[1],
+                                       2 * _cu_count(query.device), max_context_len=max_context_len,
+                                       requested_splits=num_splits))
     q, kc, vc = _prep(_pad_head_dim(query, kdim), _pad_head_dim(k_cache, kdim), _pad_head_dim(v_cache, kdim))
     out = torch.empty((batch, q_heads, kdim), dtype=query.dtype, device=query.device)
     workspace = torch.empty(_native.decode_workspace_bytes(batch, q_heads, 1, kdim, splits),
