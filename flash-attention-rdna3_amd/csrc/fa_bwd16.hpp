@@ -13,6 +13,8 @@
 //    P = exp2(s*c - lse2) is 0 there without a select.
 #pragma once
 
+#include <type_traits>
+
 #include "fa_internal.hpp"
 #include "fa_tiles.hpp"
 
@@ -37,8 +39,14 @@ struct Dkdv16Cfg {
   static constexpr int NDB = D / 32;
 };
 
+#ifndef FA_DKDV_OCC
+#define FA_DKDV_OCC 1
+#endif
+#ifndef FA_DQ_OCC
+#define FA_DQ_OCC 2
+#endif
 template <typename Tag, int D, int MODE>
-__global__ __launch_bounds__(256) void dkdv16_kernel(fa_bwd_params p, int num_n_blocks) {
+__global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params p, int num_n_blocks) {
   using C = Dkdv16Cfg<D>;
   using EL = Elem<Tag>;
   using S = uint16_t;
@@ -61,6 +69,7 @@ __global__ __launch_bounds__(256) void dkdv16_kernel(fa_bwd_params p, int num_n_
     bounded_seq(f.cu_seqlens_k, b, f.total_k, k_start, sk);
   }
   const int n0 = nblk * C::BN;
+  FA_TRACE(0);
   if (n0 >= sk || num_n_blocks <= 0) return;
 
   const S* kbase = reinterpret_cast<const S*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1] +
@@ -91,7 +100,9 @@ __global__ __launch_bounds__(256) void dkdv16_kernel(fa_bwd_params p, int num_n_
 #pragma unroll
   for (int i = 0; i < C::NDB; ++i) { dk[i] = zero16(); dv[i] = zero16(); }
 
-  SwzTile<C::BMQ, D, C::NT> qt, gt;
+  BufSwzTile<C::BMQ, D, C::NT> qt, gt;
+  qt.init(f.q_stride[2], tid);
+  gt.init(p.dout_stride[2], tid);
   const int nlast = min(n0 + C::BN, sk) - 1;
 
   for (int g = 0; g < group; ++g) {
@@ -116,8 +127,9 @@ __global__ __launch_bounds__(256) void dkdv16_kernel(fa_bwd_params p, int num_n_
 
     float lreg = 0.f, dreg = 0.f;  // this thread's lse2 / delta for the next stage
     auto load_stage = [&](int m0) {
-      qt.load([&](int r) -> const S* { int m = m0 + r; return m < sq ? qbase + (int64_t)m * qs : nullptr; }, qbase, tid);
-      gt.load([&](int r) -> const S* { int m = m0 + r; return m < sq ? gbase + (int64_t)m * gs : nullptr; }, gbase, tid);
+      const int rows = min(C::BMQ, sq - m0);
+      qt.load(rows_rsrc<D>(qbase + (int64_t)m0 * qs, qs, rows));
+      gt.load(rows_rsrc<D>(gbase + (int64_t)m0 * gs, gs, rows));
       if (tid < C::BMQ) {
         const int m = min(m0 + tid, sq - 1);
         lreg = lbase[(int64_t)m * f.lse_stride[2]];
@@ -168,32 +180,42 @@ __global__ __launch_bounds__(256) void dkdv16_kernel(fa_bwd_params p, int num_n_
 #pragma unroll
           for (int r = 0; r < 4; ++r) { l2[4 * q4 + r] = a[r]; dl[4 * q4 + r] = d[r]; }
         }
-        const bool plain = (MODE == 0) && vis == 2;
+        // The fully visible case (no modifiers) is its own straight-line
+        // body: a per-element choice would become one branch per score.
+        auto scores = [&](auto plain_t, auto cap_t, auto bias_t, auto alibi_t) {
+          constexpr bool plain = decltype(plain_t)::value;
+          constexpr bool CAP = decltype(cap_t)::value;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float pv, tc = 0.f;
-          if (plain) {
-            pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], c, -l2[i]));
-          } else {
-            const int m = m0 + acc_row(i, h);
-            const float x = score<(MODE >= 1)>(md, sacc[i], m, n, tc);
-            pv = __builtin_amdgcn_exp2f(x - l2[i]);
-            if (vis == 1 && !keep_pos(md, m, n)) pv = 0.f;
-          }
-          float dp = pacc[i], pd = pv;
-          if constexpr (MODE == 2) {
-            if (md.drop_p > 0.f) {
-              const bool keep = dropout_keep(md, m0 + acc_row(i, h), n);
-              pd = keep ? pv * md.drop_scale : 0.f;
-              dp = keep ? dp * md.drop_scale : 0.f;
+          for (int i = 0; i < 16; ++i) {
+            float pv, tc = 0.f;
+            if constexpr (plain) {
+              pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], c, -l2[i]));
+            } else {
+              const int m = m0 + acc_row(i, h);
+              const float x = score_m<CAP, decltype(bias_t)::value, decltype(alibi_t)::value>(md, sacc[i], m, n, tc);
+              pv = __builtin_amdgcn_exp2f(x - l2[i]);
+              pv = ((vis == 1) & !keep_pos(md, m, n)) ? 0.f : pv;
             }
+            float dp = pacc[i], pd = pv;
+            if constexpr (MODE == 2) {
+              if (md.drop_p > 0.f) {
+                const bool keep = dropout_keep(md, m0 + acc_row(i, h), n);
+                pd = keep ? pv * md.drop_scale : 0.f;
+                dp = keep ? dp * md.drop_scale : 0.f;
+              }
+            }
+            float ds = pv * (dp - dl[i]);
+            if constexpr (CAP) ds *= (1.f - tc * tc);
+            sacc[i] = pd;
+            pacc[i] = ds;
           }
-          float ds = pv * (dp - dl[i]);
-          if constexpr (MODE >= 1) {
-            if (md.cap2 > 0.f) ds *= (1.f - tc * tc);
-          }
-          sacc[i] = pd;
-          pacc[i] = ds;
+        };
+        using F_ = std::false_type;
+        if constexpr (MODE >= 1) {
+          dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_); });
+        } else {
+          if (vis == 2) scores(std::true_type{}, F_{}, std::integral_constant<int, 0>{}, F_{});
+          else scores(F_{}, F_{}, std::integral_constant<int, 0>{}, F_{});
         }
         s16x8 pb[C::NPV], sb[C::NPV];
 #pragma unroll
@@ -214,6 +236,7 @@ __global__ __launch_bounds__(256) void dkdv16_kernel(fa_bwd_params p, int num_n_
     }
   }
 
+  FA_TRACE(1);
   if (!nvalid) return;
   S* dkr = reinterpret_cast<S*>(p.dk) + b * p.dk_stride[0] + hk * p.dk_stride[1] +
            (int64_t)(k_start + n) * p.dk_stride[2];
@@ -255,7 +278,7 @@ struct Dq16Cfg {
 };
 
 template <typename Tag, int D, int MODE>
-__global__ __launch_bounds__(256) void dq16_kernel(fa_bwd_params p, int num_m_blocks) {
+__global__ __launch_bounds__(256, FA_DQ_OCC) void dq16_kernel(fa_bwd_params p, int num_m_blocks) {
   using C = Dq16Cfg<D>;
   using EL = Elem<Tag>;
   using S = uint16_t;
@@ -271,7 +294,8 @@ __global__ __launch_bounds__(256) void dq16_kernel(fa_bwd_params p, int num_m_bl
   const int bh = blockIdx.x - mb_rev * bh_count;
   const int b = bh / f.heads_q, hq = bh - b * f.heads_q;
   const int hk = hq / (f.heads_q / f.heads_kv);
-  const int mblk = num_m_blocks - 1 - mb_rev;
+  const int mblk = causal_block(mb_rev, num_m_blocks);
+  FA_TRACE(0);
 
   int q_start = 0, sq = f.seqlen_q, k_start = 0, sk = f.seqlen_k;
   if (f.cu_seqlens_q) {
@@ -330,10 +354,13 @@ __global__ __launch_bounds__(256) void dq16_kernel(fa_bwd_params p, int num_m_bl
 #pragma unroll
   for (int i = 0; i < C::NDB; ++i) dq[i] = zero16();
 
-  SwzTile<C::BN, D, C::NT> kt, vt;
+  BufSwzTile<C::BN, D, C::NT> kt, vt;
+  kt.init(ks, tid);
+  vt.init(vs, tid);
   auto load_stage = [&](int n0) {
-    kt.load([&](int r) -> const S* { int nn = n0 + r; return nn < sk ? kbase + (int64_t)nn * ks : nullptr; }, kbase, tid);
-    vt.load([&](int r) -> const S* { int nn = n0 + r; return nn < sk ? vbase + (int64_t)nn * vs : nullptr; }, vbase, tid);
+    const int rows = min(C::BN, sk - n0);
+    kt.load(rows_rsrc<D>(kbase + (int64_t)n0 * ks, ks, rows));
+    vt.load(rows_rsrc<D>(vbase + (int64_t)n0 * vs, vs, rows));
   };
   auto store_stage = [&](int st) {
     S* base = smem + st * C::STAGE;
@@ -364,30 +391,38 @@ __global__ __launch_bounds__(256) void dq16_kernel(fa_bwd_params p, int num_m_bl
           sacc[kb2] = EL::mma(swz_op<D>(Ks, kb2 * 32 + l32, 2 * s + h), qop[s], sacc[kb2]);
           pacc[kb2] = EL::mma(swz_op<D>(Vs, kb2 * 32 + l32, 2 * s + h), gop[s], pacc[kb2]);
         }
-      const bool plain = (MODE == 0) && vis == 2;
+      auto scores = [&](auto plain_t, auto cap_t, auto bias_t, auto alibi_t) {
+        constexpr bool plain = decltype(plain_t)::value;
+        constexpr bool CAP = decltype(cap_t)::value;
 #pragma unroll
-      for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+        for (int kb2 = 0; kb2 < C::NKB; ++kb2)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float pv, tc = 0.f;
-          const int nn = n0 + kb2 * 32 + acc_row(i, h);
-          if (plain) {
-            pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb2][i], c, -lse2));
-          } else {
-            const float x = score<(MODE >= 1)>(md, sacc[kb2][i], m, nn, tc);
-            pv = __builtin_amdgcn_exp2f(x - lse2);
-            if (vis == 1 && !keep_pos(md, m, nn)) pv = 0.f;
+          for (int i = 0; i < 16; ++i) {
+            float pv, tc = 0.f;
+            const int nn = n0 + kb2 * 32 + acc_row(i, h);
+            if constexpr (plain) {
+              pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb2][i], c, -lse2));
+            } else {
+              const float x = score_m<CAP, decltype(bias_t)::value, decltype(alibi_t)::value>(md, sacc[kb2][i], m, nn, tc);
+              pv = __builtin_amdgcn_exp2f(x - lse2);
+              pv = ((vis == 1) & !keep_pos(md, m, nn)) ? 0.f : pv;
+            }
+            float dp = pacc[kb2][i];
+            if constexpr (MODE == 2) {
+              if (md.drop_p > 0.f) dp = dropout_keep(md, m, nn) ? dp * md.drop_scale : 0.f;
+            }
+            float ds = pv * (dp - dlt);
+            if constexpr (CAP) ds *= (1.f - tc * tc);
+            sacc[kb2][i] = ds;
           }
-          float dp = pacc[kb2][i];
-          if constexpr (MODE == 2) {
-            if (md.drop_p > 0.f) dp = dropout_keep(md, m, nn) ? dp * md.drop_scale : 0.f;
-          }
-          float ds = pv * (dp - dlt);
-          if constexpr (MODE >= 1) {
-            if (md.cap2 > 0.f) ds *= (1.f - tc * tc);
-          }
-          sacc[kb2][i] = ds;
-        }
+      };
+      using F_ = std::false_type;
+      if constexpr (MODE >= 1) {
+        dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_); });
+      } else {
+        if (vis == 2) scores(std::true_type{}, F_{}, std::integral_constant<int, 0>{}, F_{});
+        else scores(F_{}, F_{}, std::integral_constant<int, 0>{}, F_{});
+      }
       s16x8 sb[C::NPV];
 #pragma unroll
       for (int j = 0; j < C::NPV; ++j) sb[j] = pack_op<Tag>(sacc[j >> 1], j & 1);
@@ -400,6 +435,7 @@ __global__ __launch_bounds__(256) void dq16_kernel(fa_bwd_params p, int num_m_bl
     __syncthreads();
   }
 
+  FA_TRACE(1);
   if (!mvalid) return;
   S* dqr = reinterpret_cast<S*>(p.dq) + b * p.dq_stride[0] + hq * p.dq_stride[1] +
            (int64_t)(q_start + m) * p.dq_stride[2];

@@ -565,6 +565,9 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
   }
   constexpr bool FAST = !std::is_same<Tag, f32_t>::value && D <= 128;
   if constexpr (FAST) {
+  const bool fast_ok = buf_rows_ok(f.q_stride[2], Dkdv16Cfg<D>::BMQ) && buf_rows_ok(p.dout_stride[2], Dkdv16Cfg<D>::BMQ) &&
+                       buf_rows_ok(f.k_stride[2], Dq16Cfg<D>::BN) && buf_rows_ok(f.v_stride[2], Dq16Cfg<D>::BN);
+  if (fast_ok) {
     if (phases & 2) {
       using C = Dkdv16Cfg<D>;
       auto kern = dkdv16_kernel<Tag, D, MODE>;
@@ -588,6 +591,7 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
+  }
   }
   if (phases & 2) {
     using C = DkdvCfg<Tag, D>;

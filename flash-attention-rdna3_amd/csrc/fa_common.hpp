@@ -15,6 +15,9 @@
 // fp32 inputs use v_mfma_f32_32x32x2_f32 (KSTEP 2, E 1).
 #pragma once
 
+#include <climits>
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -216,13 +219,18 @@ __device__ inline float tanh_fast(float y) {
   return copysignf(r, y);
 }
 
-__device__ inline bool keep_pos(const Mods& md, int m, int n) {
+// Visible keys of row m form [lo, hi] (empty when hi < lo).  The mode flags
+// are wave-uniform, so the bounds are scalar selects.
+__device__ inline void key_bounds(const Mods& md, int m, int& lo, int& hi) {
   const int qp = m + md.off;
-  bool k = n < md.seqlen_k;
-  if (md.causal) k = k && (n <= qp);
-  if (md.wl >= 0) k = k && (n >= qp - md.wl);
-  if (md.wr >= 0) k = k && (n <= qp + md.wr);
-  return k;
+  hi = min(md.seqlen_k - 1, min(md.causal ? qp : INT_MAX, md.wr >= 0 ? qp + md.wr : INT_MAX));
+  lo = md.wl >= 0 ? qp - md.wl : INT_MIN;
+}
+
+__device__ inline bool keep_pos(const Mods& md, int m, int n) {
+  int lo, hi;
+  key_bounds(md, m, lo, hi);
+  return (n <= hi) & (n >= lo);
 }
 
 __device__ inline float load_bias(const Mods& md, int m, int n) {
@@ -247,6 +255,86 @@ __device__ inline float score(const Mods& md, float s, int m, int n, float& tcap
     if (md.has_alibi) x -= md.alibi_log2 * fabsf((float)(n - m - md.off));
   }
   return x;
+}
+
+// Bias element of kind K: 1 fp32, 2 fp16, 3 bf16.
+template <int K>
+__device__ inline float load_bias_k(const Mods& md, int m, int n) {
+  const int64_t o = (int64_t)m * md.bias_sm + (int64_t)n * md.bias_sn;
+  if constexpr (K == 1) return reinterpret_cast<const float*>(md.bias)[o];
+  const uint16_t b = reinterpret_cast<const uint16_t*>(md.bias)[o];
+  if constexpr (K == 3) return Elem<bf16_t>::to_f(b);
+  return Elem<f16_t>::to_f(b);
+}
+
+// score() with the modifier set fixed at compile time (no per-score tests).
+// BIASK: 0 no bias, else the kind of load_bias_k.
+template <bool CAP, int BIASK, bool ALIBI>
+__device__ inline float score_m(const Mods& md, float s, int m, int n, float& tcap) {
+  float x = s * md.scale_log2;
+  tcap = 0.f;
+  if constexpr (CAP) {
+    tcap = tanh_fast(x / md.cap2);
+    x = md.cap2 * tcap;
+  }
+  if constexpr (BIASK != 0) x += load_bias_k<BIASK>(md, m, n) * kLog2e;
+  if constexpr (ALIBI) x -= md.alibi_log2 * fabsf((float)(n - m - md.off));
+  return x;
+}
+
+// Calls f(cap, bias_kind, alibi) with std::integral_constant flags for the
+// modifiers `md` enables: the per-tile unswitch of score_m.
+template <typename F>
+__device__ inline void dispatch_mods(const Mods& md, F&& f) {
+  using T = std::true_type;
+  using N = std::false_type;
+  auto with_bias = [&](auto cap, auto al) {
+    if (md.bias == nullptr) f(cap, std::integral_constant<int, 0>{}, al);
+    else if (md.bias_f32) f(cap, std::integral_constant<int, 1>{}, al);
+    else if (md.bias_bf16) f(cap, std::integral_constant<int, 3>{}, al);
+    else f(cap, std::integral_constant<int, 2>{}, al);
+  };
+  const bool cap = md.cap2 > 0.f, al = md.has_alibi != 0;
+  if (cap) { if (al) with_bias(T{}, T{}); else with_bias(T{}, N{}); }
+  else { if (al) with_bias(N{}, T{}); else with_bias(N{}, N{}); }
+}
+
+// Optional per-workgroup timeline for scheduling studies (build with
+// -DFA_TRACE_WG): thread 0 records start/end wall clock and its hardware
+// placement into a device array read back by fa_debug_trace_*().
+#ifdef FA_TRACE_WG
+static __device__ unsigned long long g_fa_trace[4 * 65536];
+__device__ inline void trace_wg(int slot) {
+  if (threadIdx.x != 0) return;
+  const unsigned id = blockIdx.x + blockIdx.y * gridDim.x;
+  if (id >= 65536) return;
+  volatile unsigned long long* e = g_fa_trace + 4 * id;
+  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+  if (slot == 0) {
+    e[0] = t;
+    e[2] = __builtin_amdgcn_s_getreg((4) | (0 << 6) | (31 << 11));
+    e[3] = __builtin_amdgcn_s_getreg((20) | (0 << 6) | (15 << 11));
+  } else {
+    e[1] = t;
+  }
+}
+#define FA_TRACE(slot) trace_wg(slot)
+#else
+#define FA_TRACE(slot) ((void)0)
+#endif
+
+// Order of query blocks over the grid for kernels whose block cost grows with
+// the block index (causal attention): block slot `idx` of `nb` maps to the
+// heaviest half descending, then the lightest half ascending.  When the whole
+// grid is resident at once (two workgroups per CU), the k-th and (k+G/2)-th
+// workgroups share a CU, so heavy blocks are paired with light ones.
+#ifndef FA_BLOCK_ORDER
+#define FA_BLOCK_ORDER 1
+#endif
+__device__ inline int causal_block(int idx, int nb) {
+  if (FA_BLOCK_ORDER == 0) return nb - 1 - idx;
+  const int half = (nb + 1) / 2;
+  return idx < half ? nb - 1 - idx : idx - half;
 }
 
 __device__ inline bool dropout_keep(const Mods& md, int m, int n) {

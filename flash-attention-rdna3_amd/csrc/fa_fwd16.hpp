@@ -59,7 +59,8 @@ __global__ __launch_bounds__(256, 2) void fwd16_kernel(fa_fwd_params p, int num_
   const int bh = blockIdx.x - mb_rev * bh_count;
   const int b = bh / p.heads_q, hq = bh - b * p.heads_q;
   const int hk = hq / (p.heads_q / p.heads_kv);
-  const int mblk = num_m_blocks - 1 - mb_rev;
+  const int mblk = causal_block(mb_rev, num_m_blocks);
+  FA_TRACE(0);
 
   int q_start = 0, sq = p.seqlen_q, k_start = 0, sk = p.seqlen_k;
   if (p.cu_seqlens_q) {
@@ -109,10 +110,13 @@ __global__ __launch_bounds__(256, 2) void fwd16_kernel(fa_fwd_params p, int num_
 #pragma unroll
   for (int i = 0; i < C::NDB; ++i) acc[i] = zero16();
 
-  SwzTile<C::BN, D, C::NT> kt, vt;
+  BufSwzTile<C::BN, D, C::NT> kt, vt;
+  kt.init(ks, tid);
+  vt.init(vs, tid);
   auto load_tiles = [&](int n0) {
-    kt.load([&](int r) -> const S* { int n = n0 + r; return n < sk ? kb + (int64_t)n * ks : nullptr; }, kb, tid);
-    vt.load([&](int r) -> const S* { int n = n0 + r; return n < sk ? vb + (int64_t)n * vs : nullptr; }, vb, tid);
+    const int rows = min(C::BN, sk - n0);
+    kt.load(rows_rsrc<D>(kb + (int64_t)n0 * ks, ks, rows));
+    vt.load(rows_rsrc<D>(vb + (int64_t)n0 * vs, vs, rows));
   };
   auto store_tiles = [&](int stage) {
     S* base = smem + stage * C::STAGE;
@@ -154,17 +158,25 @@ __global__ __launch_bounds__(256, 2) void fwd16_kernel(fa_fwd_params p, int num_
           for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sacc[kb2][i]);
         tmax *= c;  // the plain path is only taken for c > 0
       } else {
+        // This lane's visible keys (its row is fixed): one interval per tile.
+        int klo = INT_MIN, khi = INT_MAX;
+        if (vis == 1) key_bounds(md, m, klo, khi);
+        auto masked_scores = [&](auto cap_t, auto bias_t, auto alibi_t) {
 #pragma unroll
-        for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+          for (int kb2 = 0; kb2 < C::NKB; ++kb2)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int n = n0 + kb2 * 32 + acc_row(i, h);
-            float tc;
-            float x = score<(MODE >= 1)>(md, sacc[kb2][i], m, n, tc);
-            if (vis == 1 && !keep_pos(md, m, n)) x = kNegInf;
-            sacc[kb2][i] = x;
-            tmax = fmaxf(tmax, x);
-          }
+            for (int i = 0; i < 16; ++i) {
+              const int n = n0 + kb2 * 32 + acc_row(i, h);
+              float tc;
+              float x = score_m<decltype(cap_t)::value, decltype(bias_t)::value, decltype(alibi_t)::value>(
+                  md, sacc[kb2][i], m, n, tc);
+              x = ((n >= klo) & (n <= khi)) ? x : kNegInf;
+              sacc[kb2][i] = x;
+              tmax = fmaxf(tmax, x);
+            }
+        };
+        if constexpr (MODE >= 1) dispatch_mods(md, masked_scores);
+        else masked_scores(std::false_type{}, std::integral_constant<int, 0>{}, std::false_type{});
       }
       tmax = fmaxf(tmax, xor32(tmax));
       // Lazy rescale, decided for the whole wave.
@@ -238,6 +250,7 @@ __global__ __launch_bounds__(256, 2) void fwd16_kernel(fa_fwd_params p, int num_
     __syncthreads();
   }
 
+  FA_TRACE(1);
   if (!mvalid) return;
   const float l_safe = (l_i == 0.f) ? 1.f : l_i;
   const float inv = 1.f / l_safe;

@@ -277,6 +277,7 @@ template <typename Tag, int D, int MODE>
 static hipError_t run_fwd(const fa_fwd_params& p, hipStream_t stream) {
   if constexpr (!std::is_same<Tag, f32_t>::value && D <= 128) {
     using C = Fwd16Cfg<D>;
+    if (buf_rows_ok(p.k_stride[2], C::BN) && buf_rows_ok(p.v_stride[2], C::BN)) {
     auto kern = fwd16_kernel<Tag, D, MODE>;
     hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
     if (e != hipSuccess) return e;
@@ -285,6 +286,7 @@ static hipError_t run_fwd(const fa_fwd_params& p, hipStream_t stream) {
     if (grid <= 0) return hipSuccess;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb);
     return hipGetLastError();
+    }
   }
   using C = FwdCfg<Tag, D>;
   auto kern = fwd_kernel<Tag, D, MODE>;

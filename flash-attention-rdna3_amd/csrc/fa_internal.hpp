@@ -7,6 +7,12 @@
 
 namespace fa {
 
+// Buffer-addressed tiles use 32-bit byte offsets inside a window of `rows`
+// rows: the fast kernels need rows * stride * 2 < 2^31.
+inline bool buf_rows_ok(int64_t stride_elems, int rows) {
+  return stride_elems >= 0 && stride_elems * 2 * (int64_t)rows < (int64_t(1) << 31);
+}
+
 // Each launcher validates nothing beyond what it needs to pick a kernel
 // instantiation; fa_api.cpp has already checked the arguments.  They return
 // hipSuccess, hipErrorInvalidValue for an unsupported configuration, or the

@@ -127,6 +127,7 @@ struct TransTile {
   }
 };
 
+
 }  // namespace fa
 
 namespace fa {
@@ -216,5 +217,52 @@ __device__ inline s16x8 tr_op_rowmap(const uint16_t* tile, int rbase, int cbase,
   s16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return r;
 }
+
+// ---------------------------------------------------------------------------
+// Buffer-addressed tiles.  A buffer resource covers the valid rows of a tile
+// window (its base is rebased per tile in scalar registers); every lane's
+// byte offset inside the window is fixed, so a load is one buffer_load with a
+// constant VGPR offset, and rows past the valid range read as zero from the
+// hardware range check instead of a per-row test.  Offsets are 32-bit: the
+// host only takes these paths when R * row stride * 2 bytes < 2^31.
+// ---------------------------------------------------------------------------
+template <int COLS>
+__device__ inline __amdgpu_buffer_rsrc_t rows_rsrc(const uint16_t* row0, int64_t stride, int rows) {
+  const uint32_t bytes = rows > 0 ? (uint32_t)((int64_t)(rows - 1) * stride * 2 + COLS * 2) : 0u;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(row0), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int R, int COLS, int NT>
+struct BufSwzTile {
+  static constexpr int CPR = COLS / 8;
+  static constexpr int CH = R * CPR;
+  static constexpr int PT = (CH + NT - 1) / NT;
+  uint32_t voff[PT];
+  s16x8 r[PT];
+
+  __device__ inline void init(int64_t stride, int tid) {
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      const int c = tid + NT * j;
+      const int row = c / CPR, ch = c % CPR;
+      voff[j] = (CH % NT == 0 || c < CH) ? (uint32_t)(row * stride * 2 + ch * 16) : 0u;
+    }
+  }
+  __device__ inline void load(__amdgpu_buffer_rsrc_t rs) {
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+      r[j] = __builtin_bit_cast(s16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[j], 0, 0));
+  }
+  __device__ inline void store(uint16_t* lds, int tid) const {
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      const int c = tid + NT * j;
+      if (CH % NT == 0 || c < CH) {
+        const int row = c / CPR, ch = c % CPR;
+        *reinterpret_cast<s16x8*>(lds + row * COLS + ((ch ^ swz<COLS>(row)) << 3)) = r[j];
+      }
+    }
+  }
+};
 
 }  // namespace fa
