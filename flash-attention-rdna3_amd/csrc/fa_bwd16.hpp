@@ -25,6 +25,12 @@ __device__ inline float lse2_of(float lse) { return lse == kNegInf ? __builtin_i
 // ---------------------------------------------------------------------------
 // dK / dV: each wave owns 32 keys (lane axis of S = Q K^T).
 // ---------------------------------------------------------------------------
+#ifndef FA_DKDV_OCC
+#define FA_DKDV_OCC 1
+#endif
+#ifndef FA_DQ_OCC
+#define FA_DQ_OCC 2
+#endif
 template <int D>
 struct Dkdv16Cfg {
   static constexpr int NW = 4;
@@ -33,18 +39,17 @@ struct Dkdv16Cfg {
   static constexpr int BMQ = 32;
   static constexpr int QT = BMQ * D;                    // elements per Q / dO tile
   static constexpr int STAGE_BYTES = 2 * QT * 2 + 2 * BMQ * 4;
-  static constexpr int LDS_BYTES = 2 * STAGE_BYTES;
+  // V operands of each wave's 32 keys are parked in LDS (each lane reads back
+  // only what it wrote) instead of 32 VGPRs, so the kernel fits two waves per
+  // SIMD.
+  static constexpr bool VLDS = FA_DKDV_OCC >= 2;
+  static constexpr int VLDS_BYTES = VLDS ? NW * 32 * D * 2 : 0;
+  static constexpr int LDS_BYTES = 2 * STAGE_BYTES + VLDS_BYTES;
   static constexpr int NSTEP = D / 16;
   static constexpr int NPV = BMQ / 16;
   static constexpr int NDB = D / 32;
 };
 
-#ifndef FA_DKDV_OCC
-#define FA_DKDV_OCC 1
-#endif
-#ifndef FA_DQ_OCC
-#define FA_DQ_OCC 2
-#endif
 template <typename Tag, int D, int MODE>
 __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params p, int num_n_blocks) {
   using C = Dkdv16Cfg<D>;
@@ -95,14 +100,35 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
     }
     wait_vm_all();
   }
+  S* const vlds = reinterpret_cast<S*>(smem_raw + 2 * C::STAGE_BYTES) + wave * 32 * D;
+  if constexpr (C::VLDS) {
+#pragma unroll
+    for (int s = 0; s < C::NSTEP; ++s) *reinterpret_cast<s16x8*>(vlds + swz_off<D>(l32, 8 * (2 * s + h))) = vop[s];
+  }
+  auto vop_at = [&](int s) -> s16x8 {
+    if constexpr (C::VLDS) return swz_op<D>(vlds, l32, 2 * s + h);
+    else return vop[s];
+  };
 
   f32x16 dk[C::NDB], dv[C::NDB];
 #pragma unroll
   for (int i = 0; i < C::NDB; ++i) { dk[i] = zero16(); dv[i] = zero16(); }
 
-  BufSwzTile<C::BMQ, D, C::NT> qt, gt;
-  qt.init(f.q_stride[2], tid);
-  gt.init(p.dout_stride[2], tid);
+  // Q / dO tiles go HBM -> LDS directly when the tile is a whole number of
+  // 16-byte chunks per thread (D >= 64); otherwise through registers.
+  constexpr bool DMA = (C::BMQ * D / 8) % C::NT == 0;
+  using RegTile = BufSwzTile<C::BMQ, D, C::NT>;
+  using DTile = DmaSwzTile<C::BMQ, (DMA ? D : 64), C::NT>;
+  RegTile qt, gt;
+  DTile qd, gd;
+  if constexpr (DMA) {
+    qd.init(f.q_stride[2], tid);
+    gd.init(p.dout_stride[2], tid);
+  } else {
+    qt.init(f.q_stride[2], tid);
+    gt.init(p.dout_stride[2], tid);
+  }
+  const uint32_t lds0 = lds_addr(smem_raw);
   const int nlast = min(n0 + C::BN, sk) - 1;
 
   for (int g = 0; g < group; ++g) {
@@ -126,10 +152,16 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
     const int nsteps = mhi > mlo ? (mhi - mlo + C::BMQ - 1) / C::BMQ : 0;
 
     float lreg = 0.f, dreg = 0.f;  // this thread's lse2 / delta for the next stage
-    auto load_stage = [&](int m0) {
+    auto load_stage = [&](int m0, int st) {
       const int rows = min(C::BMQ, sq - m0);
-      qt.load(rows_rsrc<D>(qbase + (int64_t)m0 * qs, qs, rows));
-      gt.load(rows_rsrc<D>(gbase + (int64_t)m0 * gs, gs, rows));
+      if constexpr (DMA) {
+        const uint32_t base = lds0 + (uint32_t)(st * C::STAGE_BYTES);
+        qd.load(rows_rsrc_words<D>(qbase + (int64_t)m0 * qs, qs, rows), base, wave);
+        gd.load(rows_rsrc_words<D>(gbase + (int64_t)m0 * gs, gs, rows), base + C::QT * 2u, wave);
+      } else {
+        qt.load(rows_rsrc<D>(qbase + (int64_t)m0 * qs, qs, rows));
+        gt.load(rows_rsrc<D>(gbase + (int64_t)m0 * gs, gs, rows));
+      }
       if (tid < C::BMQ) {
         const int m = min(m0 + tid, sq - 1);
         lreg = lbase[(int64_t)m * f.lse_stride[2]];
@@ -139,24 +171,31 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
     auto store_stage = [&](int st, int m0) {
       unsigned char* base = smem_raw + st * C::STAGE_BYTES;
       S* sp = reinterpret_cast<S*>(base);
-      qt.store(sp, tid);
-      gt.store(sp + C::QT, tid);
+      if constexpr (!DMA) {
+        qt.store(sp, tid);
+        gt.store(sp + C::QT, tid);
+      }
       if (tid < C::BMQ) {
         float* lf = reinterpret_cast<float*>(base + 2 * C::QT * 2);
-        lf[tid] = (m0 + tid < sq) ? lse2_of(lreg) : __builtin_inff();
-        lf[C::BMQ + tid] = dreg;
+        const float l2v = (m0 + tid < sq) ? lse2_of(lreg) : __builtin_inff();
+        // MODE 0 seeds the score accumulators with -lse2/c and -delta (the
+        // MFMAs then produce s - lse2/c and dP - delta directly); the other
+        // modes need the raw scores and keep lse2 / delta.
+        lf[tid] = (MODE == 0) ? -l2v / md.scale_log2 : l2v;
+        lf[C::BMQ + tid] = (MODE == 0) ? -dreg : dreg;
       }
     };
 
     if (nsteps > 0) {
-      load_stage(mlo);
+      load_stage(mlo, 0);
       store_stage(0, mlo);
     }
+    wait_vm_all();
     __syncthreads();
     for (int t = 0; t < nsteps; ++t) {
       const int m0 = mlo + t * C::BMQ;
       const int st = t & 1;
-      if (t + 1 < nsteps) load_stage(m0 + C::BMQ);
+      if (t + 1 < nsteps) load_stage(m0 + C::BMQ, st ^ 1);
 
       const int vis = ncols > 0 ? rect_visibility(md, m0, min(C::BMQ, sq - m0), n0w, ncols) : 0;
       if (vis) {
@@ -166,19 +205,31 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
         const float* L2 = reinterpret_cast<const float*>(base + 2 * C::QT * 2);
         const float* DL = L2 + C::BMQ;
 
-        f32x16 sacc = zero16(), pacc = zero16();
-#pragma unroll
-        for (int s = 0; s < C::NSTEP; ++s) {
-          sacc = EL::mma(swz_op<D>(Qs, l32, 2 * s + h), kop[s], sacc);
-          pacc = EL::mma(swz_op<D>(Gs, l32, 2 * s + h), vop[s], pacc);
-        }
+        f32x16 sacc, pacc;
         float l2[16], dl[16];
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const f32x4 a = *reinterpret_cast<const f32x4*>(L2 + 8 * q4 + 4 * h);
           const f32x4 d = *reinterpret_cast<const f32x4*>(DL + 8 * q4 + 4 * h);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) { l2[4 * q4 + r] = a[r]; dl[4 * q4 + r] = d[r]; }
+          for (int r = 0; r < 4; ++r) {
+            if constexpr (MODE == 0) {
+              sacc[4 * q4 + r] = a[r];
+              pacc[4 * q4 + r] = d[r];
+            } else {
+              l2[4 * q4 + r] = a[r];
+              dl[4 * q4 + r] = d[r];
+            }
+          }
+        }
+        if constexpr (MODE != 0) {
+          sacc = zero16();
+          pacc = zero16();
+        }
+#pragma unroll
+        for (int s = 0; s < C::NSTEP; ++s) {
+          sacc = EL::mma(swz_op<D>(Qs, l32, 2 * s + h), kop[s], sacc);
+          pacc = EL::mma(swz_op<D>(Gs, l32, 2 * s + h), vop_at(s), pacc);
         }
         // The fully visible case (no modifiers) is its own straight-line
         // body: a per-element choice would become one branch per score.
@@ -188,8 +239,10 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             float pv, tc = 0.f;
-            if constexpr (plain) {
-              pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], c, -l2[i]));
+            if constexpr (MODE == 0) {
+              // sacc = s - lse2/c, pacc = dP - delta (seeded accumulators).
+              pv = __builtin_amdgcn_exp2f(sacc[i] * c);
+              if constexpr (!plain) pv = ((vis == 1) & !keep_pos(md, m0 + acc_row(i, h), n)) ? 0.f : pv;
             } else {
               const int m = m0 + acc_row(i, h);
               const float x = score_m<CAP, decltype(bias_t)::value, decltype(alibi_t)::value>(md, sacc[i], m, n, tc);
@@ -204,7 +257,7 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
                 dp = keep ? dp * md.drop_scale : 0.f;
               }
             }
-            float ds = pv * (dp - dl[i]);
+            float ds = (MODE == 0) ? pv * dp : pv * (dp - dl[i]);
             if constexpr (CAP) ds *= (1.f - tc * tc);
             sacc[i] = pd;
             pacc[i] = ds;
@@ -232,6 +285,7 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
           }
       }
       if (t + 1 < nsteps) store_stage(st ^ 1, m0 + C::BMQ);
+      wait_vm_all();
       __syncthreads();
     }
   }
@@ -264,13 +318,21 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
 // ---------------------------------------------------------------------------
 template <int D>
 struct Dq16Cfg {
-  static constexpr int NW = 4;
+  // 128 query rows (a row quarter of 32 per wave) with the key range split in
+  // two halves of 4 waves each, merged through LDS (same layout and reasons
+  // as the forward kernel).
+  static constexpr int NQ = 4;
+  static constexpr int NW = 2 * NQ;
   static constexpr int NT = 64 * NW;
-  static constexpr int BM = 32 * NW;
+  static constexpr int NTH = 64 * NQ;
+  static constexpr int BM = 32 * NQ;
   static constexpr int BN = (D <= 64) ? 64 : 32;
   static constexpr int KT = BN * D;
   static constexpr int STAGE = 2 * KT;  // K, V
-  static constexpr int LDS_BYTES = 2 * STAGE * 2;
+  static constexpr int HALF = 2 * STAGE;
+  static constexpr int LOOP_BYTES = 2 * HALF * 2;
+  static constexpr int MERGE_BYTES = NQ * (D / 32) * 16 * 64 * 4;
+  static constexpr int LDS_BYTES = LOOP_BYTES > MERGE_BYTES ? LOOP_BYTES : MERGE_BYTES;
   static constexpr int NSTEP = D / 16;
   static constexpr int NKB = BN / 32;
   static constexpr int NPV = BN / 16;
@@ -278,7 +340,7 @@ struct Dq16Cfg {
 };
 
 template <typename Tag, int D, int MODE>
-__global__ __launch_bounds__(256, FA_DQ_OCC) void dq16_kernel(fa_bwd_params p, int num_m_blocks) {
+__global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m_blocks) {
   using C = Dq16Cfg<D>;
   using EL = Elem<Tag>;
   using S = uint16_t;
@@ -287,14 +349,17 @@ __global__ __launch_bounds__(256, FA_DQ_OCC) void dq16_kernel(fa_bwd_params p, i
   const fa_fwd_params& f = p.fwd;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave8 = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int khalf = wave8 / C::NQ;
+  const int wave = wave8 % C::NQ;
+  const int htid = tid % C::NTH;
   const int h = lane >> 5, l32 = lane & 31;
   const int bh_count = f.batch * f.heads_q;
   const int mb_rev = blockIdx.x / bh_count;
   const int bh = blockIdx.x - mb_rev * bh_count;
   const int b = bh / f.heads_q, hq = bh - b * f.heads_q;
   const int hk = hq / (f.heads_q / f.heads_kv);
-  const int mblk = causal_block(mb_rev, num_m_blocks);
+  const int mblk = num_m_blocks - 1 - mb_rev;  // heaviest causal blocks first
   FA_TRACE(0);
 
   int q_start = 0, sq = f.seqlen_q, k_start = 0, sk = f.seqlen_k;
@@ -354,32 +419,53 @@ __global__ __launch_bounds__(256, FA_DQ_OCC) void dq16_kernel(fa_bwd_params p, i
 #pragma unroll
   for (int i = 0; i < C::NDB; ++i) dq[i] = zero16();
 
-  BufSwzTile<C::BN, D, C::NT> kt, vt;
-  kt.init(ks, tid);
-  vt.init(vs, tid);
-  auto load_stage = [&](int n0) {
+  constexpr bool DMA = (C::BN * D / 8) % C::NTH == 0;
+  BufSwzTile<C::BN, D, C::NTH> kt, vt;
+  DmaSwzTile<C::BN, (DMA ? D : 64), C::NTH> kd, vd;
+  if constexpr (DMA) {
+    kd.init(ks, htid);
+    vd.init(vs, htid);
+  } else {
+    kt.init(ks, htid);
+    vt.init(vs, htid);
+  }
+  const int nh0 = (ntiles + 1) / 2;
+  const int my_first = khalf == 0 ? 0 : nh0;
+  const int my_count = khalf == 0 ? nh0 : ntiles - nh0;
+  S* const hsmem = smem + khalf * C::HALF;
+  const uint32_t lds0 = lds_addr(hsmem);
+  auto load_stage = [&](int n0, int st) {
     const int rows = min(C::BN, sk - n0);
-    kt.load(rows_rsrc<D>(kbase + (int64_t)n0 * ks, ks, rows));
-    vt.load(rows_rsrc<D>(vbase + (int64_t)n0 * vs, vs, rows));
+    if constexpr (DMA) {
+      const uint32_t base = lds0 + (uint32_t)(st * C::STAGE) * 2u;
+      kd.load(rows_rsrc_words<D>(kbase + (int64_t)n0 * ks, ks, rows), base, wave);
+      vd.load(rows_rsrc_words<D>(vbase + (int64_t)n0 * vs, vs, rows), base + C::KT * 2u, wave);
+    } else {
+      kt.load(rows_rsrc<D>(kbase + (int64_t)n0 * ks, ks, rows));
+      vt.load(rows_rsrc<D>(vbase + (int64_t)n0 * vs, vs, rows));
+    }
   };
   auto store_stage = [&](int st) {
-    S* base = smem + st * C::STAGE;
-    kt.store(base, tid);
-    vt.store(base + C::KT, tid);
+    if constexpr (!DMA) {
+      S* base = hsmem + st * C::STAGE;
+      kt.store(base, htid);
+      vt.store(base + C::KT, htid);
+    }
   };
 
-  if (ntiles > 0) {
-    load_stage(lo);
+  if (my_count > 0) {
+    load_stage(lo + my_first * C::BN, 0);
     store_stage(0);
   }
+  wait_vm_all();
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int n0 = lo + t * C::BN;
+  for (int t = 0; t < nh0; ++t) {
+    const int n0 = lo + (my_first + t) * C::BN;
     const int st = t & 1;
-    if (t + 1 < ntiles) load_stage(n0 + C::BN);
-    const int vis = mrows > 0 ? rect_visibility(md, m0w, mrows, n0, C::BN) : 0;
+    if (t + 1 < my_count) load_stage(n0 + C::BN, st ^ 1);
+    const int vis = (mrows > 0 && t < my_count) ? rect_visibility(md, m0w, mrows, n0, C::BN) : 0;
     if (vis) {
-      const S* Ks = smem + st * C::STAGE;
+      const S* Ks = hsmem + st * C::STAGE;
       const S* Vs = Ks + C::KT;
       f32x16 sacc[C::NKB], pacc[C::NKB];
 #pragma unroll
@@ -431,8 +517,26 @@ __global__ __launch_bounds__(256, FA_DQ_OCC) void dq16_kernel(fa_bwd_params p, i
 #pragma unroll
         for (int db = 0; db < C::NDB; ++db) dq[db] = EL::mma(tr_op_rowmap<D>(Ks, 0, 32 * db, j, lane), sb[j], dq[db]);
     }
-    if (t + 1 < ntiles) store_stage(st ^ 1);
+    if (t + 1 < my_count) store_stage(st ^ 1);
+    wait_vm_all();
     __syncthreads();
+  }
+
+  // dQ = dQ(first key half) + dQ(second key half), summed in that order.
+  {
+    float* ow = reinterpret_cast<float*>(smem_raw);
+    if (khalf == 1) {
+#pragma unroll
+      for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ow[((wave * C::NDB + db) * 16 + i) * 64 + lane] = dq[db][i];
+    }
+    __syncthreads();
+    if (khalf == 1) return;
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dq[db][i] += ow[((wave * C::NDB + db) * 16 + i) * 64 + lane];
   }
 
   FA_TRACE(1);

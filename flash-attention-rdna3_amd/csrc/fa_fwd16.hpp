@@ -24,15 +24,27 @@
 
 namespace fa {
 
+// A workgroup owns BM = 128 query rows (4 row quarters of 32, one per wave)
+// and splits their key range in two: waves 0-3 stream the first half of the
+// key tiles, waves 4-7 the second, each half through its own double-buffered
+// K/V tiles.  The two partial states (O, m, l) of a row are merged through
+// LDS at the end.  One 8-wave workgroup fills a CU at two waves per SIMD, so
+// a heavy causal block runs at full CU throughput instead of sharing the CU
+// with a light one and then running alone.
 template <int D>
 struct Fwd16Cfg {
-  static constexpr int NW = 4;
+  static constexpr int NQ = 4;                 // row quarters (waves per half)
+  static constexpr int NW = 2 * NQ;
   static constexpr int NT = 64 * NW;
-  static constexpr int BM = 32 * NW;
+  static constexpr int NTH = 64 * NQ;          // threads per key half
+  static constexpr int BM = 32 * NQ;
   static constexpr int BN = 64;
   static constexpr int KTILE = BN * D;  // elements (K), then V
   static constexpr int STAGE = 2 * KTILE;
-  static constexpr int LDS_BYTES = 2 * STAGE * 2;
+  static constexpr int HALF = 2 * STAGE;       // two stages per key half
+  static constexpr int MERGE_BYTES = NQ * (D / 32) * 16 * 64 * 4 + 2 * NQ * 64 * 4;
+  static constexpr int LOOP_BYTES = 2 * HALF * 2;
+  static constexpr int LDS_BYTES = LOOP_BYTES > MERGE_BYTES ? LOOP_BYTES : MERGE_BYTES;
   static constexpr int NSTEP = D / 16;
   static constexpr int NKB = BN / 32;
   static constexpr int NPV = BN / 16;
@@ -43,7 +55,7 @@ struct Fwd16Cfg {
 constexpr float kLazyRescale = 8.0f;
 
 template <typename Tag, int D, int MODE>
-__global__ __launch_bounds__(256, 2) void fwd16_kernel(fa_fwd_params p, int num_m_blocks) {
+__global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_m_blocks) {
   using C = Fwd16Cfg<D>;
   using EL = Elem<Tag>;
   using S = uint16_t;
@@ -51,7 +63,10 @@ __global__ __launch_bounds__(256, 2) void fwd16_kernel(fa_fwd_params p, int num_
   S* smem = reinterpret_cast<S*>(smem_raw);
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave8 = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int khalf = wave8 / C::NQ;        // which half of the key tiles
+  const int wave = wave8 % C::NQ;         // row quarter
+  const int htid = tid % C::NTH;          // thread index within the key half
   const int h = lane >> 5, l32 = lane & 31;
 
   const int bh_count = p.batch * p.heads_q;
@@ -59,7 +74,7 @@ __global__ __launch_bounds__(256, 2) void fwd16_kernel(fa_fwd_params p, int num_
   const int bh = blockIdx.x - mb_rev * bh_count;
   const int b = bh / p.heads_q, hq = bh - b * p.heads_q;
   const int hk = hq / (p.heads_q / p.heads_kv);
-  const int mblk = causal_block(mb_rev, num_m_blocks);
+  const int mblk = num_m_blocks - 1 - mb_rev;  // heaviest causal blocks first
   FA_TRACE(0);
 
   int q_start = 0, sq = p.seqlen_q, k_start = 0, sk = p.seqlen_k;
@@ -110,34 +125,34 @@ __global__ __launch_bounds__(256, 2) void fwd16_kernel(fa_fwd_params p, int num_
 #pragma unroll
   for (int i = 0; i < C::NDB; ++i) acc[i] = zero16();
 
-  BufSwzTile<C::BN, D, C::NT> kt, vt;
-  kt.init(ks, tid);
-  vt.init(vs, tid);
-  auto load_tiles = [&](int n0) {
+  DmaSwzTile<C::BN, D, C::NTH> kt, vt;
+  kt.init(ks, htid);
+  vt.init(vs, htid);
+  // Key tiles [0, nh0) go to half 0, [nh0, ntiles) to half 1; both halves
+  // run nh0 steps so their barriers line up.
+  const int nh0 = (ntiles + 1) / 2;
+  const int my_first = khalf == 0 ? 0 : nh0;
+  const int my_count = khalf == 0 ? nh0 : ntiles - nh0;
+  const uint32_t lds0 = lds_addr(smem) + (uint32_t)(khalf * C::HALF) * 2u;
+  auto load_tiles = [&](int n0, int stage) {
     const int rows = min(C::BN, sk - n0);
-    kt.load(rows_rsrc<D>(kb + (int64_t)n0 * ks, ks, rows));
-    vt.load(rows_rsrc<D>(vb + (int64_t)n0 * vs, vs, rows));
-  };
-  auto store_tiles = [&](int stage) {
-    S* base = smem + stage * C::STAGE;
-    kt.store(base, tid);
-    vt.store(base + C::KTILE, tid);
+    const uint32_t base = lds0 + (uint32_t)(stage * C::STAGE) * 2u;
+    kt.load(rows_rsrc_words<D>(kb + (int64_t)n0 * ks, ks, rows), base, wave);
+    vt.load(rows_rsrc_words<D>(vb + (int64_t)n0 * vs, vs, rows), base + C::KTILE * 2u, wave);
   };
 
-  if (ntiles > 0) {
-    load_tiles(lo);
-    store_tiles(0);
-  }
+  if (my_count > 0) load_tiles(lo + my_first * C::BN, 0);
+  wait_vm_all();
   __syncthreads();
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int n0 = lo + t * C::BN;
+  for (int t = 0; t < nh0; ++t) {
+    const int n0 = lo + (my_first + t) * C::BN;
     const int stage = t & 1;
-    if (t + 1 < ntiles) load_tiles(n0 + C::BN);
+    if (t + 1 < my_count) load_tiles(n0 + C::BN, stage ^ 1);
 
-    const int vis = mrows > 0 ? rect_visibility(md, m0w, mrows, n0, C::BN) : 0;
+    const int vis = (mrows > 0 && t < my_count) ? rect_visibility(md, m0w, mrows, n0, C::BN) : 0;
     if (vis) {
-      const S* Ks = smem + stage * C::STAGE;
+      const S* Ks = smem + khalf * C::HALF + stage * C::STAGE;
       const S* Vs = Ks + C::KTILE;
       f32x16 sacc[C::NKB];
 #pragma unroll
@@ -246,8 +261,36 @@ __global__ __launch_bounds__(256, 2) void fwd16_kernel(fa_fwd_params p, int num_
         }
     }
 
-    if (t + 1 < ntiles) store_tiles(stage ^ 1);
+    wait_vm_all();
     __syncthreads();
+  }
+
+  // Merge the two key halves: half 1 parks (O^T, m, l) in LDS, half 0 folds
+  // them into its own state.  Both are relative to their own running max.
+  {
+    float* ow = reinterpret_cast<float*>(smem_raw);
+    float* mw = ow + C::NQ * C::NDB * 16 * 64;
+    float* lw = mw + C::NQ * 64;
+    if (khalf == 1) {
+#pragma unroll
+      for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ow[((wave * C::NDB + db) * 16 + i) * 64 + lane] = acc[db][i];
+      mw[wave * 64 + lane] = m_i;
+      lw[wave * 64 + lane] = l_i;
+    }
+    __syncthreads();
+    if (khalf == 1) return;
+    const float mb2 = mw[wave * 64 + lane], lb2 = lw[wave * 64 + lane];
+    const float mn = fmaxf(m_i, mb2);
+    const float mu = (mn == kNegInf) ? 0.f : mn;
+    const float sa = __builtin_amdgcn_exp2f(m_i - mu), sb = __builtin_amdgcn_exp2f(mb2 - mu);
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[db][i] = acc[db][i] * sa + ow[((wave * C::NDB + db) * 16 + i) * 64 + lane] * sb;
+    l_i = l_i * sa + lb2 * sb;
+    m_i = mn;
   }
 
   FA_TRACE(1);

@@ -265,4 +265,66 @@ struct BufSwzTile {
   }
 };
 
+// ---------------------------------------------------------------------------
+// HBM -> LDS tiles without register staging: buffer_load_dwordx4 ... lds.
+// Each instruction of a wave fills 1 KB of LDS contiguously (lane i at +16*i,
+// base in M0); each lane picks the global 16-byte chunk whose swizzled LDS
+// slot is its own, so the tile lands in the swz<COLS> layout.  The load is
+// issued from inline asm: the compiler does not track it, so it neither
+// drains it before unrelated LDS reads nor waits for it at all -- the kernel
+// waits (vmcnt) and synchronises (barrier) before reading the tile.
+// ---------------------------------------------------------------------------
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline i32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu));
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+template <int COLS>
+__device__ inline i32x4 rows_rsrc_words(const uint16_t* row0, int64_t stride, int rows) {
+  const uint32_t bytes = rows > 0 ? (uint32_t)((int64_t)(rows - 1) * stride * 2 + COLS * 2) : 0u;
+  return rsrc_words(row0, bytes);
+}
+
+__device__ inline void buf_load_lds16(i32x4 rs, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rs), "s"(lds_addr)
+               : "memory", "m0");
+}
+
+template <int R, int COLS, int NT>
+struct DmaSwzTile {
+  static constexpr int CPR = COLS / 8;
+  static constexpr int CH = R * CPR;
+  static_assert(CH % NT == 0, "tile must be a whole number of 16-byte chunks per thread");
+  static constexpr int PT = CH / NT;
+  uint32_t voff[PT];
+
+  __device__ inline void init(int64_t stride, int tid) {
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      const int slot = NT * j + tid;
+      const int row = slot / CPR;
+      const int lc = (slot % CPR) ^ swz<COLS>(row);
+      voff[j] = (uint32_t)(row * stride * 2 + lc * 16);
+    }
+  }
+  // lds_tile: byte address of the tile in LDS; wave: this wave's index.
+  __device__ inline void load(i32x4 rs, uint32_t lds_tile, int wave) const {
+#pragma unroll
+    for (int j = 0; j < PT; ++j) buf_load_lds16(rs, voff[j], lds_tile + (uint32_t)(NT * j + 64 * wave) * 16u);
+  }
+};
+
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 }  // namespace fa

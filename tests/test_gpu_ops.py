@@ -191,8 +191,11 @@ def test_dropout_backward_consistency():
     out, lse = _forward(q, k, v, False, scale, (-1, -1), 0.0, None, None, p, seed)
     dq, dk, dv = _backward(do, q, k, v, out, lse, False, scale, (-1, -1), 0.0, None, None, p, seed)
     base = (out.float() * do.float()).sum()
-    eps = 0.1
     for grad, name in ((dq, "q"), (dk, "k"), (dv, "v")):
+        # O is linear in V, so a large step there has no truncation error and
+        # lifts the difference above the fp16 rounding of O; Q and K need a
+        # small step.
+        eps = 2.0 if name == "v" else 0.1
         direction = torch.randn_like(q)
         t = {"q": q, "k": k, "v": v}
         t[name] = t[name] + eps * direction
