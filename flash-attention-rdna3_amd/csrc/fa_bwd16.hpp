@@ -25,33 +25,38 @@ __device__ inline float lse2_of(float lse) { return lse == kNegInf ? __builtin_i
 // ---------------------------------------------------------------------------
 // dK / dV: each wave owns 32 keys (lane axis of S = Q K^T).
 // ---------------------------------------------------------------------------
-#ifndef FA_DKDV_OCC
-#define FA_DKDV_OCC 1
-#endif
 #ifndef FA_DQ_OCC
 #define FA_DQ_OCC 2
 #endif
+// A workgroup owns BN = 128 keys (32 per wave of a half) and splits their
+// query range in two: waves 0-3 walk the first half of the query steps,
+// waves 4-7 the second, each half through its own double-buffered Q / dO
+// stages.  The K and V operands of the 128 keys are parked once in LDS (they
+// are shared by the two waves that own the same keys), which keeps a wave
+// under 256 VGPRs so the 8-wave workgroup runs at two waves per SIMD.  The
+// two dK / dV partial sums are added through LDS at the end in a fixed order.
 template <int D>
 struct Dkdv16Cfg {
-  static constexpr int NW = 4;
+  static constexpr int NQ = 4;                          // key quarters (waves per half)
+  static constexpr int NW = 2 * NQ;
   static constexpr int NT = 64 * NW;
-  static constexpr int BN = 32 * NW;
+  static constexpr int NTH = 64 * NQ;
+  static constexpr int BN = 32 * NQ;
   static constexpr int BMQ = 32;
   static constexpr int QT = BMQ * D;                    // elements per Q / dO tile
   static constexpr int STAGE_BYTES = 2 * QT * 2 + 2 * BMQ * 4;
-  // V operands of each wave's 32 keys are parked in LDS (each lane reads back
-  // only what it wrote) instead of 32 VGPRs, so the kernel fits two waves per
-  // SIMD.
-  static constexpr bool VLDS = FA_DKDV_OCC >= 2;
-  static constexpr int VLDS_BYTES = VLDS ? NW * 32 * D * 2 : 0;
-  static constexpr int LDS_BYTES = 2 * STAGE_BYTES + VLDS_BYTES;
+  static constexpr int HALF_BYTES = 2 * STAGE_BYTES;
+  static constexpr int PARK_BYTES = 2 * BN * D * 2;     // K then V, [key quarter][32][D]
+  static constexpr int LOOP_BYTES = 2 * HALF_BYTES + PARK_BYTES;
+  static constexpr int MERGE_BYTES = NQ * 2 * (D / 32) * 16 * 64 * 4;
+  static constexpr int LDS_BYTES = LOOP_BYTES > MERGE_BYTES ? LOOP_BYTES : MERGE_BYTES;
   static constexpr int NSTEP = D / 16;
   static constexpr int NPV = BMQ / 16;
   static constexpr int NDB = D / 32;
 };
 
 template <typename Tag, int D, int MODE>
-__global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params p, int num_n_blocks) {
+__global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num_n_blocks) {
   using C = Dkdv16Cfg<D>;
   using EL = Elem<Tag>;
   using S = uint16_t;
@@ -59,7 +64,10 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
   const fa_fwd_params& f = p.fwd;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave8 = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qhalf = wave8 / C::NQ;        // which half of the query steps
+  const int wave = wave8 % C::NQ;         // key quarter
+  const int htid = tid % C::NTH;
   const int h = lane >> 5, l32 = lane & 31;
   const int bhk_count = f.batch * f.heads_kv;
   // Low key blocks first: under causal masking they see the most query rows.
@@ -85,50 +93,49 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
   const int ncols = min(32, sk - n0w);
   const int n = n0w + l32;
   const bool nvalid = n < sk;
-  s16x8 kop[C::NSTEP], vop[C::NSTEP];
-  {
+
+  // Park this key quarter's K / V operands (the lane layout of the MFMA B
+  // operand) in LDS; the first barrier of the query loop publishes them.
+  S* const klds = reinterpret_cast<S*>(smem_raw + 2 * C::HALF_BYTES) + wave * 32 * D;
+  S* const vlds = klds + C::BN * D;
+  if (qhalf == 0) {
     const S* kr = kbase + (int64_t)(nvalid ? n : 0) * f.k_stride[2] + 8 * h;
     const S* vr = vbase + (int64_t)(nvalid ? n : 0) * f.v_stride[2] + 8 * h;
+    s16x8 kop[C::NSTEP], vop[C::NSTEP];
 #pragma unroll
     for (int s = 0; s < C::NSTEP; ++s) {
       kop[s] = load_op<Tag>(kr + 16 * s);
       vop[s] = load_op<Tag>(vr + 16 * s);
     }
-    if (!nvalid) {
-#pragma unroll
-      for (int s = 0; s < C::NSTEP; ++s) { kop[s] = zero_op<Tag>(); vop[s] = zero_op<Tag>(); }
-    }
     wait_vm_all();
-  }
-  S* const vlds = reinterpret_cast<S*>(smem_raw + 2 * C::STAGE_BYTES) + wave * 32 * D;
-  if constexpr (C::VLDS) {
 #pragma unroll
-    for (int s = 0; s < C::NSTEP; ++s) *reinterpret_cast<s16x8*>(vlds + swz_off<D>(l32, 8 * (2 * s + h))) = vop[s];
+    for (int s = 0; s < C::NSTEP; ++s) {
+      const int off = swz_off<D>(l32, 8 * (2 * s + h));
+      *reinterpret_cast<s16x8*>(klds + off) = nvalid ? kop[s] : zero_op<Tag>();
+      *reinterpret_cast<s16x8*>(vlds + off) = nvalid ? vop[s] : zero_op<Tag>();
+    }
   }
-  auto vop_at = [&](int s) -> s16x8 {
-    if constexpr (C::VLDS) return swz_op<D>(vlds, l32, 2 * s + h);
-    else return vop[s];
-  };
 
   f32x16 dk[C::NDB], dv[C::NDB];
 #pragma unroll
   for (int i = 0; i < C::NDB; ++i) { dk[i] = zero16(); dv[i] = zero16(); }
 
   // Q / dO tiles go HBM -> LDS directly when the tile is a whole number of
-  // 16-byte chunks per thread (D >= 64); otherwise through registers.
-  constexpr bool DMA = (C::BMQ * D / 8) % C::NT == 0;
-  using RegTile = BufSwzTile<C::BMQ, D, C::NT>;
-  using DTile = DmaSwzTile<C::BMQ, (DMA ? D : 64), C::NT>;
+  // 16-byte chunks per thread of a half (D >= 64); otherwise through registers.
+  constexpr bool DMA = (C::BMQ * D / 8) % C::NTH == 0;
+  using RegTile = BufSwzTile<C::BMQ, D, C::NTH>;
+  using DTile = DmaSwzTile<C::BMQ, (DMA ? D : 64), C::NTH>;
   RegTile qt, gt;
   DTile qd, gd;
   if constexpr (DMA) {
-    qd.init(f.q_stride[2], tid);
-    gd.init(p.dout_stride[2], tid);
+    qd.init(f.q_stride[2], htid);
+    gd.init(p.dout_stride[2], htid);
   } else {
-    qt.init(f.q_stride[2], tid);
-    gt.init(p.dout_stride[2], tid);
+    qt.init(f.q_stride[2], htid);
+    gt.init(p.dout_stride[2], htid);
   }
-  const uint32_t lds0 = lds_addr(smem_raw);
+  unsigned char* const hsmem = smem_raw + qhalf * C::HALF_BYTES;
+  const uint32_t lds0 = lds_addr(hsmem);
   const int nlast = min(n0 + C::BN, sk) - 1;
 
   for (int g = 0; g < group; ++g) {
@@ -150,6 +157,11 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
     if (f.window_left >= 0) mhi = min(mhi, nlast - md.off + f.window_left + 1);
     mlo = max(mlo, 0) / C::BMQ * C::BMQ;
     const int nsteps = mhi > mlo ? (mhi - mlo + C::BMQ - 1) / C::BMQ : 0;
+    // Query steps [0, nh0) go to half 0, [nh0, nsteps) to half 1; both
+    // halves run nh0 iterations so their barriers line up.
+    const int nh0 = (nsteps + 1) / 2;
+    const int my_first = qhalf == 0 ? 0 : nh0;
+    const int my_count = qhalf == 0 ? nh0 : nsteps - nh0;
 
     float lreg = 0.f, dreg = 0.f;  // this thread's lse2 / delta for the next stage
     auto load_stage = [&](int m0, int st) {
@@ -162,44 +174,45 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
         qt.load(rows_rsrc<D>(qbase + (int64_t)m0 * qs, qs, rows));
         gt.load(rows_rsrc<D>(gbase + (int64_t)m0 * gs, gs, rows));
       }
-      if (tid < C::BMQ) {
-        const int m = min(m0 + tid, sq - 1);
+      if (htid < C::BMQ) {
+        const int m = min(m0 + htid, sq - 1);
         lreg = lbase[(int64_t)m * f.lse_stride[2]];
         dreg = dbase[(int64_t)m * p.delta_stride[2]];
       }
     };
     auto store_stage = [&](int st, int m0) {
-      unsigned char* base = smem_raw + st * C::STAGE_BYTES;
+      unsigned char* base = hsmem + st * C::STAGE_BYTES;
       S* sp = reinterpret_cast<S*>(base);
       if constexpr (!DMA) {
-        qt.store(sp, tid);
-        gt.store(sp + C::QT, tid);
+        qt.store(sp, htid);
+        gt.store(sp + C::QT, htid);
       }
-      if (tid < C::BMQ) {
+      if (htid < C::BMQ) {
         float* lf = reinterpret_cast<float*>(base + 2 * C::QT * 2);
-        const float l2v = (m0 + tid < sq) ? lse2_of(lreg) : __builtin_inff();
+        const float l2v = (m0 + htid < sq) ? lse2_of(lreg) : __builtin_inff();
         // MODE 0 seeds the score accumulators with -lse2/c and -delta (the
         // MFMAs then produce s - lse2/c and dP - delta directly); the other
         // modes need the raw scores and keep lse2 / delta.
-        lf[tid] = (MODE == 0) ? -l2v / md.scale_log2 : l2v;
-        lf[C::BMQ + tid] = (MODE == 0) ? -dreg : dreg;
+        lf[htid] = (MODE == 0) ? -l2v / md.scale_log2 : l2v;
+        lf[C::BMQ + htid] = (MODE == 0) ? -dreg : dreg;
       }
     };
 
-    if (nsteps > 0) {
-      load_stage(mlo, 0);
-      store_stage(0, mlo);
+    if (my_count > 0) {
+      const int m_first = mlo + my_first * C::BMQ;
+      load_stage(m_first, 0);
+      store_stage(0, m_first);
     }
     wait_vm_all();
     __syncthreads();
-    for (int t = 0; t < nsteps; ++t) {
-      const int m0 = mlo + t * C::BMQ;
+    for (int t = 0; t < nh0; ++t) {
+      const int m0 = mlo + (my_first + t) * C::BMQ;
       const int st = t & 1;
-      if (t + 1 < nsteps) load_stage(m0 + C::BMQ, st ^ 1);
+      if (t + 1 < my_count) load_stage(m0 + C::BMQ, st ^ 1);
 
-      const int vis = ncols > 0 ? rect_visibility(md, m0, min(C::BMQ, sq - m0), n0w, ncols) : 0;
+      const int vis = (ncols > 0 && t < my_count) ? rect_visibility(md, m0, min(C::BMQ, sq - m0), n0w, ncols) : 0;
       if (vis) {
-        const unsigned char* base = smem_raw + st * C::STAGE_BYTES;
+        const unsigned char* base = hsmem + st * C::STAGE_BYTES;
         const S* Qs = reinterpret_cast<const S*>(base);
         const S* Gs = Qs + C::QT;
         const float* L2 = reinterpret_cast<const float*>(base + 2 * C::QT * 2);
@@ -228,8 +241,8 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
         }
 #pragma unroll
         for (int s = 0; s < C::NSTEP; ++s) {
-          sacc = EL::mma(swz_op<D>(Qs, l32, 2 * s + h), kop[s], sacc);
-          pacc = EL::mma(swz_op<D>(Gs, l32, 2 * s + h), vop_at(s), pacc);
+          sacc = EL::mma(swz_op<D>(Qs, l32, 2 * s + h), swz_op<D>(klds, l32, 2 * s + h), sacc);
+          pacc = EL::mma(swz_op<D>(Gs, l32, 2 * s + h), swz_op<D>(vlds, l32, 2 * s + h), pacc);
         }
         // The fully visible case (no modifiers) is its own straight-line
         // body: a per-element choice would become one branch per score.
@@ -284,10 +297,34 @@ __global__ __launch_bounds__(256, FA_DKDV_OCC) void dkdv16_kernel(fa_bwd_params 
             dk[db] = EL::mma(tr_op_rowmap<D>(Qs, 0, 32 * db, j, lane), sb[j], dk[db]);
           }
       }
-      if (t + 1 < nsteps) store_stage(st ^ 1, m0 + C::BMQ);
+      if (t + 1 < my_count) store_stage(st ^ 1, m0 + C::BMQ);
       wait_vm_all();
       __syncthreads();
     }
+  }
+
+  // dK / dV = first query half + second query half, added in that order.
+  {
+    float* ow = reinterpret_cast<float*>(smem_raw);
+    __syncthreads();  // the parked operands and stages are dead from here
+    if (qhalf == 1) {
+#pragma unroll
+      for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          ow[(((wave * 2 + 0) * C::NDB + db) * 16 + i) * 64 + lane] = dk[db][i];
+          ow[(((wave * 2 + 1) * C::NDB + db) * 16 + i) * 64 + lane] = dv[db][i];
+        }
+    }
+    __syncthreads();
+    if (qhalf == 1) return;
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        dk[db][i] += ow[(((wave * 2 + 0) * C::NDB + db) * 16 + i) * 64 + lane];
+        dv[db][i] += ow[(((wave * 2 + 1) * C::NDB + db) * 16 + i) * 64 + lane];
+      }
   }
 
   FA_TRACE(1);
