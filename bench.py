@@ -33,6 +33,12 @@ import torch  # noqa: E402
 PEAK_FP16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 
+# HBM bytes moved per dkdv16_kernel<f16,128,0> launch at config 2, from
+# rocprofv3 FETCH_SIZE / WRITE_SIZE runs scaled by a 256 MiB copy
+# (profiles/cfg2_hbm_traffic.md).  The bench cannot read counters itself;
+# re-measure when the kernel changes.
+DKDV_TRAFFIC_BYTES = 110.4e6
+
 CFG2 = dict(batch=2, heads=16, seqlen=2048, head_dim=128, causal=True, dtype=torch.float16)
 
 
@@ -148,6 +154,9 @@ def run_cfg2(steps, warmup):
     v.requires_grad_(True)
 
     def step():
+        # As after optimizer.zero_grad(set_to_none=True): the gradients are
+        # written, not added into earlier ones (no extra elementwise kernels).
+        q.grad = k.grad = v.grad = None
         out = flash_attention(q, k, v, causal=True, softmax_scale=scale)
         out.backward(do)
 
@@ -181,7 +190,7 @@ def dkdv_roofline(tensors, iters=50):
     achieved = flops / (ms * 1e-3) / 1e12
     return {"kernel": "dkdv16_kernel<f16,128,0>", "bound": "mfma", "achieved": round(achieved, 2),
             "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-            "traffic": None, "avg_us": round(ms * 1e3, 2), "flops_per_launch": flops}
+            "traffic": DKDV_TRAFFIC_BYTES, "avg_us": round(ms * 1e3, 2), "flops_per_launch": flops}
 
 
 def run_decode_configs(iters=50):
@@ -229,6 +238,7 @@ def run_cfg5(iters=5):
     mx = max(lengths)
 
     def step():
+        q.grad = k.grad = v.grad = None
         out = flash_attention_varlen(q, k, v, cu, cu, mx, mx, causal=True, window_size=(1024, -1), softcap=50.0)
         out.backward(do)
 
