@@ -194,7 +194,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
         // MFMAs then produce s - lse2/c and dP - delta directly); the other
         // modes need the raw scores and keep lse2 / delta.
         lf[htid] = (MODE == 0) ? -l2v / md.scale_log2 : l2v;
-        lf[C::BMQ + htid] = (MODE == 0) ? -dreg : dreg;
+        lf[C::BMQ + htid] = (MODE != 2) ? -dreg : dreg;
       }
     };
 
@@ -219,26 +219,23 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
         const float* DL = L2 + C::BMQ;
 
         f32x16 sacc, pacc;
-        float l2[16], dl[16];
+        float dl[16];
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const f32x4 a = *reinterpret_cast<const f32x4*>(L2 + 8 * q4 + 4 * h);
           const f32x4 d = *reinterpret_cast<const f32x4*>(DL + 8 * q4 + 4 * h);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            if constexpr (MODE == 0) {
-              sacc[4 * q4 + r] = a[r];
-              pacc[4 * q4 + r] = d[r];
-            } else {
-              l2[4 * q4 + r] = a[r];
-              dl[4 * q4 + r] = d[r];
-            }
+            // The dP accumulator starts at -delta except under dropout (whose
+            // dP is scaled per score first); the score accumulator starts at
+            // -lse2/c in MODE 0, where no modifier needs the raw score.
+            if constexpr (MODE == 0) sacc[4 * q4 + r] = a[r];
+            if constexpr (MODE != 2) pacc[4 * q4 + r] = d[r];
+            else dl[4 * q4 + r] = d[r];
           }
         }
-        if constexpr (MODE != 0) {
-          sacc = zero16();
-          pacc = zero16();
-        }
+        if constexpr (MODE != 0) sacc = zero16();
+        if constexpr (MODE == 2) pacc = zero16();
 #pragma unroll
         for (int s = 0; s < C::NSTEP; ++s) {
           sacc = EL::mma(swz_op<D>(Qs, l32, 2 * s + h), swz_op<D>(klds, l32, 2 * s + h), sacc);
@@ -259,7 +256,10 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
             } else {
               const int m = m0 + acc_row(i, h);
               const float x = score_m<CAP, decltype(bias_t)::value, decltype(alibi_t)::value>(md, sacc[i], m, n, tc);
-              pv = __builtin_amdgcn_exp2f(x - l2[i]);
+              // lse2 of this score's row, read here rather than held across
+              // the stage (register pressure of the modifier variants).
+              const float l2i = L2[8 * (i / 4) + 4 * h + (i % 4)];
+              pv = __builtin_amdgcn_exp2f(x - l2i);
               pv = ((vis == 1) & !keep_pos(md, m, n)) ? 0.f : pv;
             }
             float dp = pacc[i], pd = pv;
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
                 dp = keep ? dp * md.drop_scale : 0.f;
               }
             }
-            float ds = (MODE == 0) ? pv * dp : pv * (dp - dl[i]);
+            float ds = (MODE != 2) ? pv * dp : pv * (dp - dl[i]);
             if constexpr (CAP) ds *= (1.f - tc * tc);
             sacc[i] = pd;
             pacc[i] = ds;

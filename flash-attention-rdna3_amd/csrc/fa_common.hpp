@@ -195,6 +195,7 @@ __device__ inline float philox_uniform(uint64_t seed, uint64_t offset) {
 struct Mods {
   float scale_log2;   // softmax_scale * log2(e)
   float cap2;         // softcap * log2(e), 0 = off
+  float inv_cap2;     // 1 / cap2 (0 when off)
   const void* bias;   // already offset to (batch, head); NULL = off
   int bias_f32;       // bias element type: 1 fp32, 0 q dtype
   int bias_bf16;      // q dtype is bf16 (only meaningful when !bias_f32)
@@ -212,10 +213,10 @@ struct Mods {
 };
 
 __device__ inline float tanh_fast(float y) {
-  // tanh(y) = sign(y) * (1 - e^{-2|y|}) / (1 + e^{-2|y|}), e^{-2|y|} <= 1.
-  float a = fabsf(y);
-  float t = __expf(-2.f * a);
-  float r = (1.f - t) / (1.f + t);
+  // tanh(y) = sign(y) * (1 - e^{-2|y|}) / (1 + e^{-2|y|}), e^{-2|y|} <= 1:
+  // hardware exp2 and reciprocal (about 1 ulp each), no division sequence.
+  const float t = __builtin_amdgcn_exp2f(fabsf(y) * (-2.0f * kLog2e));
+  const float r = (1.f - t) * __builtin_amdgcn_rcpf(1.f + t);
   return copysignf(r, y);
 }
 
@@ -248,7 +249,7 @@ __device__ inline float score(const Mods& md, float s, int m, int n, float& tcap
   tcap = 0.f;
   if constexpr (MODS) {
     if (md.cap2 > 0.f) {
-      tcap = tanh_fast(x / md.cap2);
+      tcap = tanh_fast(x * md.inv_cap2);
       x = md.cap2 * tcap;
     }
     if (md.bias) x += load_bias(md, m, n) * kLog2e;
@@ -274,7 +275,7 @@ __device__ inline float score_m(const Mods& md, float s, int m, int n, float& tc
   float x = s * md.scale_log2;
   tcap = 0.f;
   if constexpr (CAP) {
-    tcap = tanh_fast(x / md.cap2);
+    tcap = tanh_fast(x * md.inv_cap2);
     x = md.cap2 * tcap;
   }
   if constexpr (BIASK != 0) x += load_bias_k<BIASK>(md, m, n) * kLog2e;
@@ -373,6 +374,7 @@ __device__ inline Mods make_mods(const fa_fwd_params& p, int b, int hq, int sq, 
   Mods md;
   md.scale_log2 = p.softmax_scale * kLog2e;
   md.cap2 = p.softcap * kLog2e;
+  md.inv_cap2 = md.cap2 > 0.f ? 1.f / md.cap2 : 0.f;
   md.bias = nullptr;
   md.bias_f32 = p.bias_dtype == FA_DTYPE_F32;
   md.bias_bf16 = p.dtype == FA_DTYPE_BF16;
