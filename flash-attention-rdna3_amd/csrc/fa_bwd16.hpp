@@ -198,6 +198,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
       }
     };
 
+    const VisBounds kvb = key_block_bounds(md, n0w, ncols);
     if (my_count > 0) {
       const int m_first = mlo + my_first * C::BMQ;
       load_stage(m_first, 0);
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
       const int st = t & 1;
       if (t + 1 < my_count) load_stage(m0 + C::BMQ, st ^ 1);
 
-      const int vis = (ncols > 0 && t < my_count) ? rect_visibility(md, m0, min(C::BMQ, sq - m0), n0w, ncols) : 0;
+      const int vis = t < my_count ? bounds_vis(kvb, m0 + md.off, min(m0 + C::BMQ, sq) - 1 + md.off) : 0;
       if (vis) {
         const unsigned char* base = hsmem + st * C::STAGE_BYTES;
         const S* Qs = reinterpret_cast<const S*>(base);
@@ -490,6 +491,7 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
     }
   };
 
+  const VisBounds qvb = row_block_bounds(md, m0w, mrows);
   if (my_count > 0) {
     load_stage(lo + my_first * C::BN, 0);
     store_stage(0);
@@ -500,7 +502,7 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
     const int n0 = lo + (my_first + t) * C::BN;
     const int st = t & 1;
     if (t + 1 < my_count) load_stage(n0 + C::BN, st ^ 1);
-    const int vis = (mrows > 0 && t < my_count) ? rect_visibility(md, m0w, mrows, n0, C::BN) : 0;
+    const int vis = t < my_count ? bounds_vis(qvb, n0, n0 + C::BN - 1) : 0;
     if (vis) {
       const S* Ks = hsmem + st * C::STAGE;
       const S* Vs = Ks + C::KT;

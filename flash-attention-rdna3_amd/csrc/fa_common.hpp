@@ -359,6 +359,53 @@ __device__ inline int rect_visibility(const Mods& md, int m0, int mr, int n0, in
   return full ? 2 : 1;
 }
 
+// Tile visibility from per-block bounds computed once.  For a fixed block of
+// query rows (positions q = m + off in [q0, q1]) a key tile [n0, n1] is
+// visible (1) when it meets [lo_any, hi_any] and fully visible (2) when it
+// lies inside [lo_all, hi_all]; same result as rect_visibility, with the
+// mode tests hoisted out of the tile loop.
+struct VisBounds {
+  int lo_any, hi_any, lo_all, hi_all;
+};
+
+__device__ inline VisBounds row_block_bounds(const Mods& md, int m0, int mr) {
+  VisBounds v;
+  if (mr <= 0) {
+    v.lo_any = INT_MAX; v.hi_any = INT_MIN; v.lo_all = INT_MAX; v.hi_all = INT_MIN;
+    return v;
+  }
+  const int q0 = m0 + md.off, q1 = m0 + mr - 1 + md.off;
+  v.lo_any = md.wl >= 0 ? q0 - md.wl : INT_MIN;
+  v.hi_any = min(md.seqlen_k - 1, min(md.causal ? q1 : INT_MAX, md.wr >= 0 ? q1 + md.wr : INT_MAX));
+  v.lo_all = md.wl >= 0 ? q1 - md.wl : INT_MIN;
+  v.hi_all = min(md.seqlen_k - 1, min(md.causal ? q0 : INT_MAX, md.wr >= 0 ? q0 + md.wr : INT_MAX));
+  return v;
+}
+
+// The transposed case: fixed keys [n0, n1], query tiles varying.  Bounds are
+// on the query position q = m + off.
+__device__ inline VisBounds key_block_bounds(const Mods& md, int n0, int nc) {
+  VisBounds v;
+  const int n1 = n0 + nc - 1;
+  if (nc <= 0 || n0 >= md.seqlen_k) {
+    v.lo_any = INT_MAX; v.hi_any = INT_MIN; v.lo_all = INT_MAX; v.hi_all = INT_MIN;
+    return v;
+  }
+  v.lo_any = max(md.causal ? n0 : INT_MIN, md.wr >= 0 ? n0 - md.wr : INT_MIN);
+  v.hi_any = md.wl >= 0 ? n1 + md.wl : INT_MAX;
+  const bool keys_ok = n1 < md.seqlen_k;
+  v.lo_all = keys_ok ? max(md.causal ? n1 : INT_MIN, md.wr >= 0 ? n1 - md.wr : INT_MIN) : INT_MAX;
+  v.hi_all = keys_ok ? (md.wl >= 0 ? n0 + md.wl : INT_MAX) : INT_MIN;
+  return v;
+}
+
+// 0 / 1 / 2 for the interval [a0, a1] against the bounds.
+__device__ inline int bounds_vis(const VisBounds& v, int a0, int a1) {
+  const bool any = (a1 >= v.lo_any) & (a0 <= v.hi_any);
+  const bool all = (a0 >= v.lo_all) & (a1 <= v.hi_all);
+  return any ? (all ? 2 : 1) : 0;
+}
+
 // Bounded varlen interval (reference varlen.py:21-27).
 __device__ inline void bounded_seq(const int32_t* cu, int b, int total, int& start, int& len) {
   int s = cu[b], e = cu[b + 1];

@@ -134,23 +134,31 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
   const int my_first = khalf == 0 ? 0 : nh0;
   const int my_count = khalf == 0 ? nh0 : ntiles - nh0;
   const uint32_t lds0 = lds_addr(smem) + (uint32_t)(khalf * C::HALF) * 2u;
-  auto load_tiles = [&](int n0, int stage) {
-    const int rows = min(C::BN, sk - n0);
+  // Tile sources advance by BN rows per load (scalar pointer arithmetic).
+  int n_next = lo + my_first * C::BN;
+  const S* k_next = kb + (int64_t)n_next * ks;
+  const S* v_next = vb + (int64_t)n_next * vs;
+  auto load_tiles = [&](int stage) {
+    const int rows = min(C::BN, sk - n_next);
     const uint32_t base = lds0 + (uint32_t)(stage * C::STAGE) * 2u;
-    kt.load(rows_rsrc_words<D>(kb + (int64_t)n0 * ks, ks, rows), base, wave);
-    vt.load(rows_rsrc_words<D>(vb + (int64_t)n0 * vs, vs, rows), base + C::KTILE * 2u, wave);
+    kt.load(rows_rsrc_words<D>(k_next, ks, rows), base, wave);
+    vt.load(rows_rsrc_words<D>(v_next, vs, rows), base + C::KTILE * 2u, wave);
+    n_next += C::BN;
+    k_next += (int64_t)C::BN * ks;
+    v_next += (int64_t)C::BN * vs;
   };
+  const VisBounds vbnd = row_block_bounds(md, m0w, mrows);
 
-  if (my_count > 0) load_tiles(lo + my_first * C::BN, 0);
+  if (my_count > 0) load_tiles(0);
   wait_vm_all();
   __syncthreads();
 
   for (int t = 0; t < nh0; ++t) {
     const int n0 = lo + (my_first + t) * C::BN;
     const int stage = t & 1;
-    if (t + 1 < my_count) load_tiles(n0 + C::BN, stage ^ 1);
+    if (t + 1 < my_count) load_tiles(stage ^ 1);
 
-    const int vis = (mrows > 0 && t < my_count) ? rect_visibility(md, m0w, mrows, n0, C::BN) : 0;
+    const int vis = t < my_count ? bounds_vis(vbnd, n0, n0 + C::BN - 1) : 0;
     if (vis) {
       const S* Ks = smem + khalf * C::HALF + stage * C::STAGE;
       const S* Vs = Ks + C::KTILE;

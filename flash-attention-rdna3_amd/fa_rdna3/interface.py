@@ -341,6 +341,30 @@ def _flash_fwd_backward(ctx, grad_out, grad_lse):
 _flash_fwd.register_autograd(_flash_fwd_backward, setup_context=_flash_fwd_setup_context)
 
 
+class _FlashAttentionEager(torch.autograd.Function):
+    """Eager-mode twin of ``fa_rdna3::flash_fwd`` + its registered autograd:
+    same launches, without the custom-op dispatch layers (whose Python cost
+    per call is comparable to the kernels at training sizes).  Traced code
+    (torch.compile) goes through the op."""
+
+    @staticmethod
+    def forward(ctx, query, key, value, causal, softmax_scale, window_left, window_right,
+                softcap, bias, alibi, dropout_p, dropout_seed):
+        out, lse = _forward(query, key, value, causal, softmax_scale, (window_left, window_right),
+                            softcap, bias, alibi, dropout_p, dropout_seed)
+        ctx.save_for_backward(query, key, value, out, lse, bias, alibi)
+        ctx.args = (causal, softmax_scale, (window_left, window_right), softcap, dropout_p, dropout_seed)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        query, key, value, out, lse, bias, alibi = ctx.saved_tensors
+        causal, softmax_scale, window, softcap, dropout_p, dropout_seed = ctx.args
+        dq, dk, dv = _backward(grad_out.contiguous(), query, key, value, out, lse, causal, softmax_scale,
+                               window, softcap, bias, alibi, dropout_p, dropout_seed)
+        return dq, dk, dv, None, None, None, None, None, None, None, None, None
+
+
 # ---------------------------------------------------------------------------
 # Tiny fp32 inference op (reference interface.py:84-104, :336-352)
 # ---------------------------------------------------------------------------
@@ -443,8 +467,12 @@ def flash_attention(query, key, value, causal=False, softmax_scale=None, window_
         value = torch.nn.functional.pad(value, (0, pad))
 
     dropout_seed = int(torch.randint(0, 2 ** 31 - 1, (1,)).item()) if dropout_p > 0.0 else 0
-    out, _ = _flash_fwd(query, key, value, causal, softmax_scale, window_size[0], window_size[1],
-                        softcap, bias, alibi_slopes, dropout_p, dropout_seed)
+    if torch.compiler.is_compiling():
+        out, _ = _flash_fwd(query, key, value, causal, softmax_scale, window_size[0], window_size[1],
+                            softcap, bias, alibi_slopes, dropout_p, dropout_seed)
+    else:
+        out = _FlashAttentionEager.apply(query, key, value, causal, softmax_scale, window_size[0],
+                                         window_size[1], softcap, bias, alibi_slopes, dropout_p, dropout_seed)
     if pad:
         out = out[..., :head_dim]
     return out
