@@ -242,6 +242,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
           sacc = EL::mma(swz_op<D>(Qs, l32, 2 * s + h), swz_op<D>(klds, l32, 2 * s + h), sacc);
           pacc = EL::mma(swz_op<D>(Gs, l32, 2 * s + h), swz_op<D>(vlds, l32, 2 * s + h), pacc);
         }
+        if constexpr (MODE == 0) sched_read_ahead<2 * C::NSTEP, 4, 2, 8>();
         // The fully visible case (no modifiers) is its own straight-line
         // body: a per-element choice would become one branch per score.
         auto scores = [&](auto plain_t, auto cap_t, auto bias_t, auto alibi_t) {
@@ -297,6 +298,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
             dv[db] = EL::mma(tr_op_rowmap<D>(Gs, 0, 32 * db, j, lane), pb[j], dv[db]);
             dk[db] = EL::mma(tr_op_rowmap<D>(Qs, 0, 32 * db, j, lane), sb[j], dk[db]);
           }
+        if constexpr (MODE == 0) sched_read_ahead<2 * C::NPV * C::NDB, 4, 2>();
       }
       if (t + 1 < my_count) store_stage(st ^ 1, m0 + C::BMQ);
       wait_vm_all();
@@ -516,6 +518,7 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
           sacc[kb2] = EL::mma(swz_op<D>(Ks, kb2 * 32 + l32, 2 * s + h), qop[s], sacc[kb2]);
           pacc[kb2] = EL::mma(swz_op<D>(Vs, kb2 * 32 + l32, 2 * s + h), gop[s], pacc[kb2]);
         }
+      if constexpr (MODE == 0) sched_read_ahead<2 * C::NSTEP * C::NKB, 4>();
       auto scores = [&](auto plain_t, auto cap_t, auto bias_t, auto alibi_t) {
         constexpr bool plain = decltype(plain_t)::value;
         constexpr bool CAP = decltype(cap_t)::value;
@@ -555,6 +558,7 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
       for (int j = 0; j < C::NPV; ++j)
 #pragma unroll
         for (int db = 0; db < C::NDB; ++db) dq[db] = EL::mma(tr_op_rowmap<D>(Ks, 0, 32 * db, j, lane), sb[j], dq[db]);
+      if constexpr (MODE == 0) sched_read_ahead<C::NPV * C::NDB, 4, 2>();
     }
     if (t + 1 < my_count) store_stage(st ^ 1);
     wait_vm_all();

@@ -170,6 +170,7 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
 #pragma unroll
         for (int kb2 = 0; kb2 < C::NKB; ++kb2)
           sacc[kb2] = EL::mma(swz_op<D>(Ks, kb2 * 32 + l32, 2 * s + h), qop[s], sacc[kb2]);
+      sched_read_ahead<C::NSTEP * C::NKB, 4>();
 
       // Scores -> log2 domain (masked or modified when needed), tile max.
       float tmax = kNegInf;
@@ -267,6 +268,7 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
           acc[db] = EL::mma(a, pb[j], acc[db]);
           if constexpr (PSPLIT) acc[db] = EL::mma(a, pl[j], acc[db]);
         }
+      if constexpr (!PSPLIT) sched_read_ahead<C::NPV * C::NDB, 4, 2>();
     }
 
     wait_vm_all();

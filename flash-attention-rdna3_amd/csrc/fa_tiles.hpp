@@ -327,4 +327,22 @@ __device__ inline uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// Scheduling hint for a block of N MFMAs that each consume RPM LDS reads:
+// issue the reads of the first AHEAD MFMAs first, then alternate one MFMA
+// with the reads of a later one, so LDS latency overlaps MFMA execution
+// instead of each MFMA waiting on its own reads.  (sched_group_barrier
+// masks: 0x008 MFMA, 0x100 DS read.)
+// EXTRA: further LDS reads at the head of the block (e.g. accumulator seeds).
+template <int N, int AHEAD, int RPM = 1, int EXTRA = 0>
+__device__ inline void sched_read_ahead() {
+  constexpr int A = AHEAD < N ? AHEAD : N;
+  __builtin_amdgcn_sched_group_barrier(0x100, A * RPM + EXTRA, 0);
+#pragma unroll
+  for (int i = 0; i < N - A; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, RPM, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, A, 0);
+}
+
 }  // namespace fa
