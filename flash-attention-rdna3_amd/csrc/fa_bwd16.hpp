@@ -380,7 +380,7 @@ struct Dq16Cfg {
 };
 
 template <typename Tag, int D, int MODE>
-__global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m_blocks) {
+__global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m_blocks, int fuse_delta) {
   using C = Dq16Cfg<D>;
   using EL = Elem<Tag>;
   using S = uint16_t;
@@ -438,13 +438,37 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
                   (int64_t)(q_start + mm) * f.q_stride[2] + 8 * h;
     const S* gr = reinterpret_cast<const S*>(p.dout) + b * p.dout_stride[0] + hq * p.dout_stride[1] +
                   (int64_t)(q_start + mm) * p.dout_stride[2] + 8 * h;
+    // With fuse_delta, O is loaded in the same chunks as dO (issued with the
+    // operand loads, one round trip) for delta = rowsum(O * dO).
+    const S* orow = reinterpret_cast<const S*>(fuse_delta ? f.out : f.q) +
+                    (fuse_delta ? b * f.out_stride[0] + hq * f.out_stride[1] + (int64_t)(q_start + mm) * f.out_stride[2]
+                                : b * f.q_stride[0] + hq * f.q_stride[1] + (int64_t)(q_start + mm) * f.q_stride[2]) +
+                    8 * h;
+    s16x8 oop[C::NSTEP];
 #pragma unroll
     for (int s = 0; s < C::NSTEP; ++s) {
       qop[s] = load_op<Tag>(qr + 16 * s);
       gop[s] = load_op<Tag>(gr + 16 * s);
+      oop[s] = load_op<Tag>(orow + 16 * s);
     }
     const float l = f.lse[b * f.lse_stride[0] + hq * f.lse_stride[1] + (int64_t)(q_start + mm) * f.lse_stride[2]];
-    const float d = p.delta[b * p.delta_stride[0] + hq * p.delta_stride[1] + (int64_t)(q_start + mm) * p.delta_stride[2]];
+    float* const drow = p.delta + b * p.delta_stride[0] + hq * p.delta_stride[1] + (int64_t)(q_start + mm) * p.delta_stride[2];
+    float d;
+    if (fuse_delta) {
+      // delta = rowsum(O * dO) for this lane's row, from the same 16-byte
+      // chunks the dO operand holds (reference backward.py:18-46); written
+      // for the dK/dV kernel, which runs after this one.
+      wait_vm_all();
+      float acc = 0.f;
+#pragma unroll
+      for (int s = 0; s < C::NSTEP; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += EL::to_f((uint16_t)oop[s][e]) * EL::to_f((uint16_t)gop[s][e]);
+      d = acc + xor32(acc);
+      if (mvalid && khalf == 0 && h == 0) *drow = d;
+    } else {
+      d = *drow;
+    }
     wait_vm_all();
     if (mvalid) {
       lse2 = lse2_of(l);

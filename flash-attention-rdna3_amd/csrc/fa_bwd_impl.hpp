@@ -557,17 +557,33 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(fa_bwd_params p, int num_m_
 template <typename Tag, int D, int MODE>
 static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream) {
   const fa_fwd_params& f = p.fwd;
-  if (phases & 1) {
+  constexpr bool FAST = !std::is_same<Tag, f32_t>::value && D <= 128;
+  bool fast_ok = false;
+  if constexpr (FAST)
+    fast_ok = buf_rows_ok(f.q_stride[2], Dkdv16Cfg<D>::BMQ) && buf_rows_ok(p.dout_stride[2], Dkdv16Cfg<D>::BMQ) &&
+              buf_rows_ok(f.k_stride[2], Dq16Cfg<D>::BN) && buf_rows_ok(f.v_stride[2], Dq16Cfg<D>::BN);
+  // The full 16-bit backward computes delta inside the dQ kernel, which then
+  // runs first; otherwise delta has its own kernel.
+  const bool fused_delta = fast_ok && (phases & 1) && (phases & 4);
+  if ((phases & 1) && !fused_delta) {
     dim3 grid((f.seqlen_q + 15) / 16, f.batch * f.heads_q);
     hipLaunchKernelGGL((bwd_delta_kernel<Tag, D>), grid, dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  constexpr bool FAST = !std::is_same<Tag, f32_t>::value && D <= 128;
   if constexpr (FAST) {
-  const bool fast_ok = buf_rows_ok(f.q_stride[2], Dkdv16Cfg<D>::BMQ) && buf_rows_ok(p.dout_stride[2], Dkdv16Cfg<D>::BMQ) &&
-                       buf_rows_ok(f.k_stride[2], Dq16Cfg<D>::BN) && buf_rows_ok(f.v_stride[2], Dq16Cfg<D>::BN);
   if (fast_ok) {
+    if (phases & 4) {
+      using C = Dq16Cfg<D>;
+      auto kern = dq16_kernel<Tag, D, MODE>;
+      hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
+      if (e != hipSuccess) return e;
+      const int nmb = (f.seqlen_q + C::BM - 1) / C::BM;
+      const long grid = (long)nmb * f.batch * f.heads_q;
+      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb, fused_delta ? 1 : 0);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
     if (phases & 2) {
       using C = Dkdv16Cfg<D>;
       auto kern = dkdv16_kernel<Tag, D, MODE>;
@@ -576,17 +592,6 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
       const int nnb = (f.seqlen_k + C::BN - 1) / C::BN;
       const long grid = (long)nnb * f.batch * f.heads_kv;
       hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nnb);
-      e = hipGetLastError();
-      if (e != hipSuccess) return e;
-    }
-    if (phases & 4) {
-      using C = Dq16Cfg<D>;
-      auto kern = dq16_kernel<Tag, D, MODE>;
-      hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
-      if (e != hipSuccess) return e;
-      const int nmb = (f.seqlen_q + C::BM - 1) / C::BM;
-      const long grid = (long)nmb * f.batch * f.heads_q;
-      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
