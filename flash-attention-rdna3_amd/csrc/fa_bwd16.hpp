@@ -464,7 +464,7 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
       for (int s = 0; s < C::NSTEP; ++s)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc += EL::to_f((uint16_t)oop[s][e]) * EL::to_f((uint16_t)gop[s][e]);
-      d = acc + xor32(acc);
+      d = half_sum(acc);
       if (mvalid && khalf == 0 && h == 0) *drow = d;
     } else {
       d = *drow;

@@ -162,7 +162,19 @@ __device__ inline void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 // ---------------------------------------------------------------------------
 // Cross-lane helpers (wave64).
 // ---------------------------------------------------------------------------
-__device__ inline float xor32(float x) { return __shfl_xor(x, 32, 64); }
+// x combined with its partner lane 32 apart (sum / max over the two wave
+// halves), without an LDS round trip: v_permlane32_swap exchanges the upper
+// half of its first operand with the lower half of its second, so with both
+// operands = x the pair holds x's lower half twice (r[0]) and its upper half
+// twice (r[1]), and r[0] op r[1] is the combined value in every lane.
+__device__ inline float half_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float half_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
 // ---------------------------------------------------------------------------
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as easy

@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
         sacc[i] = x;
         tmax = fmaxf(tmax, x);
       }
-      tmax = fmaxf(tmax, xor32(tmax));
+      tmax = half_max(tmax);
       const float m_new = fmaxf(m_i, tmax);
       const float m_use = (m_new == kNegInf) ? 0.f : m_new;
       const float alpha = exp2f(m_i - m_use);
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
         sacc[i] = pv;
         rsum += pv;
       }
-      rsum += xor32(rsum);
+      rsum = half_sum(rsum);
       l_i = l_i * alpha + rsum;
       m_i = m_new;
       constexpr int J = 16 / EL::E;

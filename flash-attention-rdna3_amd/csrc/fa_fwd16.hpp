@@ -156,9 +156,8 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
   for (int t = 0; t < nh0; ++t) {
     const int n0 = lo + (my_first + t) * C::BN;
     const int stage = t & 1;
-    if (t + 1 < my_count) load_tiles(stage ^ 1);
-
     const int vis = t < my_count ? bounds_vis(vbnd, n0, n0 + C::BN - 1) : 0;
+    if (!vis && t + 1 < my_count) load_tiles(stage ^ 1);
     if (vis) {
       const S* Ks = smem + khalf * C::HALF + stage * C::STAGE;
       const S* Vs = Ks + C::KTILE;
@@ -171,6 +170,9 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
         for (int kb2 = 0; kb2 < C::NKB; ++kb2)
           sacc[kb2] = EL::mma(swz_op<D>(Ks, kb2 * 32 + l32, 2 * s + h), qop[s], sacc[kb2]);
       sched_read_ahead<C::NSTEP * C::NKB, 4>();
+      // The next tile's loads go out while the score MFMAs drain (issuing
+      // them before the MFMAs would hold the MFMAs back behind the queue).
+      if (t + 1 < my_count) load_tiles(stage ^ 1);
 
       // Scores -> log2 domain (masked or modified when needed), tile max.
       float tmax = kNegInf;
@@ -202,7 +204,7 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
         if constexpr (MODE >= 1) dispatch_mods(md, masked_scores);
         else masked_scores(std::false_type{}, std::integral_constant<int, 0>{}, std::false_type{});
       }
-      tmax = fmaxf(tmax, xor32(tmax));
+      tmax = half_max(tmax);
       // Lazy rescale, decided for the whole wave.
       if (__builtin_amdgcn_ballot_w64(tmax > m_i + kLazyRescale)) {
         const float m_new = fmaxf(m_i, tmax);
@@ -234,7 +236,7 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
             rsum += pv;
           }
       }
-      rsum += xor32(rsum);
+      rsum = half_sum(rsum);
       l_i += rsum;
       if constexpr (MODE == 2) {
         if (md.drop_p > 0.f) {

@@ -184,7 +184,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(fa_fwd_params p, int num_m_blo
           tmax = fmaxf(tmax, x);
         }
       }
-      tmax = fmaxf(tmax, xor32(tmax));
+      tmax = half_max(tmax);
       const float m_new = fmaxf(m_i, tmax);
       const float m_use = (m_new == kNegInf) ? 0.f : m_new;  // safe softmax
       const float alpha = exp2f(m_i - m_use);
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(fa_fwd_params p, int num_m_blo
           rsum += pv;
         }
       }
-      rsum += xor32(rsum);
+      rsum = half_sum(rsum);
       l_i = l_i * alpha + rsum;
       m_i = m_new;
 #pragma unroll
