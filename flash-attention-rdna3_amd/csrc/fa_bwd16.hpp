@@ -312,22 +312,18 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
     __syncthreads();  // the parked operands and stages are dead from here
     if (qhalf == 1) {
 #pragma unroll
-      for (int db = 0; db < C::NDB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          ow[(((wave * 2 + 0) * C::NDB + db) * 16 + i) * 64 + lane] = dk[db][i];
-          ow[(((wave * 2 + 1) * C::NDB + db) * 16 + i) * 64 + lane] = dv[db][i];
-        }
+      for (int db = 0; db < C::NDB; ++db) {
+        park_acc(ow + ((wave * 2 + 0) * C::NDB + db) * 1024, lane, dk[db]);
+        park_acc(ow + ((wave * 2 + 1) * C::NDB + db) * 1024, lane, dv[db]);
+      }
     }
     __syncthreads();
     if (qhalf == 1) return;
 #pragma unroll
-    for (int db = 0; db < C::NDB; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        dk[db][i] += ow[(((wave * 2 + 0) * C::NDB + db) * 16 + i) * 64 + lane];
-        dv[db][i] += ow[(((wave * 2 + 1) * C::NDB + db) * 16 + i) * 64 + lane];
-      }
+    for (int db = 0; db < C::NDB; ++db) {
+      dk[db] += unpark_acc(ow + ((wave * 2 + 0) * C::NDB + db) * 1024, lane);
+      dv[db] += unpark_acc(ow + ((wave * 2 + 1) * C::NDB + db) * 1024, lane);
+    }
   }
 
   FA_TRACE(1);
@@ -594,16 +590,12 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
     float* ow = reinterpret_cast<float*>(smem_raw);
     if (khalf == 1) {
 #pragma unroll
-      for (int db = 0; db < C::NDB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) ow[((wave * C::NDB + db) * 16 + i) * 64 + lane] = dq[db][i];
+      for (int db = 0; db < C::NDB; ++db) park_acc(ow + (wave * C::NDB + db) * 1024, lane, dq[db]);
     }
     __syncthreads();
     if (khalf == 1) return;
 #pragma unroll
-    for (int db = 0; db < C::NDB; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) dq[db][i] += ow[((wave * C::NDB + db) * 16 + i) * 64 + lane];
+    for (int db = 0; db < C::NDB; ++db) dq[db] += unpark_acc(ow + (wave * C::NDB + db) * 1024, lane);
   }
 
   FA_TRACE(1);

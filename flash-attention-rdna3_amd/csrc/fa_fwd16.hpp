@@ -285,9 +285,7 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
     float* lw = mw + C::NQ * 64;
     if (khalf == 1) {
 #pragma unroll
-      for (int db = 0; db < C::NDB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) ow[((wave * C::NDB + db) * 16 + i) * 64 + lane] = acc[db][i];
+      for (int db = 0; db < C::NDB; ++db) park_acc(ow + (wave * C::NDB + db) * 1024, lane, acc[db]);
       mw[wave * 64 + lane] = m_i;
       lw[wave * 64 + lane] = l_i;
     }
@@ -298,9 +296,11 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
     const float mu = (mn == kNegInf) ? 0.f : mn;
     const float sa = __builtin_amdgcn_exp2f(m_i - mu), sb = __builtin_amdgcn_exp2f(mb2 - mu);
 #pragma unroll
-    for (int db = 0; db < C::NDB; ++db)
+    for (int db = 0; db < C::NDB; ++db) {
+      const f32x16 o2 = unpark_acc(ow + (wave * C::NDB + db) * 1024, lane);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[db][i] = acc[db][i] * sa + ow[((wave * C::NDB + db) * 16 + i) * 64 + lane] * sb;
+      for (int i = 0; i < 16; ++i) acc[db][i] = acc[db][i] * sa + o2[i] * sb;
+    }
     l_i = l_i * sa + lb2 * sb;
     m_i = mn;
   }

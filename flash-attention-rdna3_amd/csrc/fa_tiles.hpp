@@ -345,4 +345,28 @@ __device__ inline void sched_read_ahead() {
   __builtin_amdgcn_sched_group_barrier(0x008, A, 0);
 }
 
+
+// A 32x32 fp32 accumulator (16 values per lane) parked in LDS and read back
+// as four 16-byte chunks per lane, chunk-major (chunk c of lane L at float
+// offset (64 * c + L) * 4), so every ds_write_b128 / ds_read_b128 of a wave
+// covers 1 KiB of consecutive addresses.  A block takes 1024 floats.
+__device__ inline void park_acc(float* blk, int lane, const f32x16& a) {
+  f32x4* p = reinterpret_cast<f32x4*>(blk);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) p[64 * c + lane] = f32x4{a[4 * c], a[4 * c + 1], a[4 * c + 2], a[4 * c + 3]};
+}
+__device__ inline f32x16 unpark_acc(const float* blk, int lane) {
+  const f32x4* p = reinterpret_cast<const f32x4*>(blk);
+  f32x16 a;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const f32x4 v = p[64 * c + lane];
+    a[4 * c] = v[0];
+    a[4 * c + 1] = v[1];
+    a[4 * c + 2] = v[2];
+    a[4 * c + 3] = v[3];
+  }
+  return a;
+}
+
 }  // namespace fa
