@@ -105,6 +105,13 @@ def cfg3_bytes(lens):
     return sum(int(n) for n in lens) * 8 * 128 * 2 * 2 + 2 * 4 * 32 * 128 * 2
 
 
+def kvcache_bytes(lens, snew=4):
+    """cfg3's cache read at lengths len_b + snew, the appended rows written
+    (and read from the inputs), q and out (Sq = snew)."""
+    return (sum(int(n) + snew for n in lens) * 8 * 128 * 2 * 2 + 2 * 4 * 8 * snew * 128 * 2 * 2
+            + 2 * 4 * 32 * snew * 128 * 2)
+
+
 def cfg4_bytes():
     return 4 * 16384 * 8 * 128 * 2 * 2 + 4 * 1024 * 4 + 2 * 4 * 32 * 128 * 2
 
@@ -194,7 +201,7 @@ def dkdv_roofline(tensors, iters=50):
 
 
 def run_decode_configs(iters=50):
-    from fa_rdna3 import flash_attention_decode, flash_attention_decode_paged
+    from fa_rdna3 import flash_attention_decode, flash_attention_decode_paged, flash_attention_with_kvcache
 
     res = {}
     stream = torch.cuda.current_stream()
@@ -212,6 +219,25 @@ def run_decode_configs(iters=50):
         gb = cfg3_bytes(lens.tolist()) / (ms * 1e-3) / 1e9
         res["cfg3_splitk_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
                                      "frac_hbm": round(gb / PEAK_HBM_GBS, 4), "caches_flushed": "read of 512 MiB"}
+        # KV-cache entry point on the cfg3 cache: 4 new tokens per sequence
+        # appended in place at the cfg3 lengths, then 4 query rows attend
+        # bottom-right causally (speculative / chunked decode step).
+        g = _gen(1)
+        q4 = torch.randn(4, 32, 4, 128, generator=g).half().cuda()
+        kn = torch.randn(4, 8, 4, 128, generator=g).half().cuda()
+        vn = torch.randn(4, 8, 4, 128, generator=g).half().cuda()
+        fk = lambda: flash_attention_with_kvcache(q4, k, v, kn, vn, cache_seqlens=lens, causal=True)
+        for _ in range(5):
+            fk()
+        tot = 0.0
+        for _ in range(iters):
+            _flush(flush)
+            tot += _event_time(fk, 1, stream)
+        ms = tot / iters
+        gb = kvcache_bytes(lens.tolist()) / (ms * 1e-3) / 1e9
+        res["kvcache_append_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
+                                        "frac_hbm": round(gb / PEAK_HBM_GBS, 4), "caches_flushed": "read of 512 MiB",
+                                        "shape": "cfg3 cache, Sq = Snew = 4, causal"}
         del q, k, v
         q, kc, vc, bt, ctx = workload_cfg4()
         f4 = lambda: flash_attention_decode_paged(q, kc, vc, bt, ctx, max_context_len=16384)

@@ -106,6 +106,7 @@ size_t fa_params_size(int which) {
     case 2: return sizeof(fa_decode_params);
     case 3: return sizeof(fa_paged_params);
     case 4: return sizeof(fa_tiny_params);
+    case 5: return sizeof(fa_append_params);
   }
   return 0;
 }
@@ -157,6 +158,7 @@ int fa_decode_splitk(const fa_decode_params* params, void* stream) {
       !rows_ok(p.out, p.out_stride, 4, 2))
     return fail(FA_ERR_INVALID, "fa_decode_splitk: q/k/v/out need a unit last stride and 16-byte aligned rows");
   if (!p.workspace || !aligned16(p.workspace)) return fail(FA_ERR_INVALID, "fa_decode_splitk: workspace");
+  if (p.causal != 0 && p.causal != 1) return fail(FA_ERR_INVALID, "fa_decode_splitk: causal must be 0 or 1");
   return from_hip(fa::launch_decode(p, (hipStream_t)stream), "fa_decode_splitk");
 }
 
@@ -187,6 +189,24 @@ int fa_tiny_fwd_f32(const fa_tiny_params* params, void* stream) {
     return fail(FA_ERR_INVALID, "fa_tiny_fwd_f32: bad shape");
   if (!p.q || !p.k || !p.v || !p.out) return fail(FA_ERR_INVALID, "fa_tiny_fwd_f32: NULL tensor");
   return from_hip(fa::launch_tiny(p, (hipStream_t)stream), "fa_tiny_fwd_f32");
+}
+
+int fa_kvcache_append(const fa_append_params* params, void* stream) {
+  if (!params) return fail(FA_ERR_INVALID, "fa_kvcache_append: params is NULL");
+  const fa_append_params& p = *params;
+  if (p.abi_version != FA_ABI_VERSION) return fail(FA_ERR_INVALID, "fa_kvcache_append: abi_version mismatch");
+  if (p.dtype != FA_DTYPE_F16 && p.dtype != FA_DTYPE_BF16)
+    return fail(FA_ERR_INVALID, "fa_kvcache_append: dtype must be f16 or bf16");
+  if (p.head_dim <= 0 || p.head_dim % 8)
+    return fail(FA_ERR_UNSUPPORTED, "fa_kvcache_append: head_dim %d not a multiple of 8", p.head_dim);
+  if (p.batch <= 0 || p.heads_kv <= 0 || p.seqlen_new < 0 || p.seqlen_cache <= 0)
+    return fail(FA_ERR_INVALID, "fa_kvcache_append: bad shape");
+  if (!p.cache_seqlens) return fail(FA_ERR_INVALID, "fa_kvcache_append: cache_seqlens is NULL");
+  if (p.seqlen_new == 0) return FA_OK;
+  if (!rows_ok(p.k_new, p.k_new_stride, 4, 2) || !rows_ok(p.v_new, p.v_new_stride, 4, 2) ||
+      !rows_ok(p.k_cache, p.k_cache_stride, 4, 2) || !rows_ok(p.v_cache, p.v_cache_stride, 4, 2))
+    return fail(FA_ERR_INVALID, "fa_kvcache_append: tensors need a unit last stride and 16-byte aligned rows");
+  return from_hip(fa::launch_append(p, (hipStream_t)stream), "fa_kvcache_append");
 }
 
 }  // extern "C"

@@ -45,10 +45,12 @@ struct DecodeArgs {
   int32_t block_shift;  // log2(block_size)
   const int32_t* lens;  // NULL: every sequence has max_len keys
   int64_t lens_stride;
+  int32_t lens_add;     // added to lens[b] before clamping
   int32_t max_len;      // Sk, or max_blocks * block_size when paged
   int32_t batch, heads_q, heads_kv, seqlen_q, head_dim;
   float scale_log2;
   int32_t num_splits;
+  int32_t causal;       // bottom-right per sequence: row i sees keys <= len - Sq + i
   float* ws_o;          // [splits][B][Hq][Sq][D] fp32
   float* ws_lse;        // [splits][B][Hq][Sq] fp32
 };
@@ -110,7 +112,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   const int dc = blockIdx.z;
 
   int len = a.max_len;
-  if (a.lens) len = min(max(a.lens[b * a.lens_stride], 0), a.max_len);
+  if (a.lens) len = min(max(a.lens[b * a.lens_stride] + a.lens_add, 0), a.max_len);
   const int nch = (len + C::CH - 1) / C::CH;
   const int per = nch / a.num_splits, extra = nch % a.num_splits;
   const int c0 = split * per + min(split, extra);
@@ -124,6 +126,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   const int hq = hk * group + g;
   const S* qrow = reinterpret_cast<const S*>(a.q) + b * a.q_stride[0] + hq * a.q_stride[1] +
                   mq * a.q_stride[2] + EL::E * h;
+  // Last key this lane's query row sees (bottom-right causal), or all.
+  const int klim = a.causal ? len - a.seqlen_q + mq : INT_MAX;
   Op qop[C::QREG ? C::NSTEP : 1];
   if constexpr (C::QREG) {
 #pragma unroll
@@ -196,10 +200,11 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
         sacc = EL::mma(load_op<Tag>(krow + EL::KSTEP * s), bq, sacc);
       }
       float tmax = kNegInf;
+      const int n0c = (c0 + my) * C::CH;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int kr = acc_row(i, h);
-        const float x = ((valid_cur >> kr) & 1u) ? sacc[i] * a.scale_log2 : kNegInf;
+        const float x = (((valid_cur >> kr) & 1u) && n0c + kr <= klim) ? sacc[i] * a.scale_log2 : kNegInf;
         sacc[i] = x;
         tmax = fmaxf(tmax, x);
       }
@@ -378,6 +383,7 @@ hipError_t launch_decode(const fa_decode_params& p, hipStream_t s) {
   for (int i = 0; i < 3; ++i) { a.k_stride[i] = p.k_stride[i]; a.v_stride[i] = p.v_stride[i]; }
   a.lens = p.cache_seqlens;
   a.lens_stride = p.cache_seqlens_stride;
+  a.lens_add = p.cache_seqlens_add;
   a.max_len = p.seqlen_k;
   a.batch = p.batch;
   a.heads_q = p.heads_q;
@@ -386,6 +392,7 @@ hipError_t launch_decode(const fa_decode_params& p, hipStream_t s) {
   a.head_dim = p.head_dim;
   a.scale_log2 = p.softmax_scale * kLog2e;
   a.num_splits = p.num_splits;
+  a.causal = p.causal ? 1 : 0;
   split_workspace(a, p.workspace);
   return decode_dispatch<false>(p.dtype, a, s);
 }
@@ -424,6 +431,42 @@ hipError_t launch_paged(const fa_paged_params& p, hipStream_t s) {
   a.num_splits = p.num_splits;
   split_workspace(a, p.workspace);
   return decode_dispatch<true>(p.dtype, a, s);
+}
+
+
+// ---------------------------------------------------------------------------
+// KV-cache append (cache update of the kv-cache entry point): one 16-byte
+// piece of a new K and V row per thread, written at row cache_seqlens[b] + s.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void kv_append_kernel(fa_append_params p, int64_t pieces) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= pieces) return;
+  const int cpr = p.head_dim / 8;  // 16-byte pieces per row
+  const int c = (int)(i % cpr);
+  int64_t row = i / cpr;
+  const int s = (int)(row % p.seqlen_new);
+  row /= p.seqlen_new;
+  const int h = (int)(row % p.heads_kv);
+  const int b = (int)(row / p.heads_kv);
+  const int pos = p.cache_seqlens[b * p.cache_seqlens_stride] + s;
+  if (pos < 0 || pos >= p.seqlen_cache) return;
+  const uint16_t* kn = reinterpret_cast<const uint16_t*>(p.k_new) + b * p.k_new_stride[0] + h * p.k_new_stride[1] +
+                       (int64_t)s * p.k_new_stride[2] + 8 * c;
+  const uint16_t* vn = reinterpret_cast<const uint16_t*>(p.v_new) + b * p.v_new_stride[0] + h * p.v_new_stride[1] +
+                       (int64_t)s * p.v_new_stride[2] + 8 * c;
+  uint16_t* kc = reinterpret_cast<uint16_t*>(p.k_cache) + b * p.k_cache_stride[0] + h * p.k_cache_stride[1] +
+                 (int64_t)pos * p.k_cache_stride[2] + 8 * c;
+  uint16_t* vc = reinterpret_cast<uint16_t*>(p.v_cache) + b * p.v_cache_stride[0] + h * p.v_cache_stride[1] +
+                 (int64_t)pos * p.v_cache_stride[2] + 8 * c;
+  *reinterpret_cast<uint4*>(kc) = *reinterpret_cast<const uint4*>(kn);
+  *reinterpret_cast<uint4*>(vc) = *reinterpret_cast<const uint4*>(vn);
+}
+
+hipError_t launch_append(const fa_append_params& p, hipStream_t stream) {
+  const int64_t pieces = (int64_t)p.batch * p.heads_kv * p.seqlen_new * (p.head_dim / 8);
+  if (pieces == 0) return hipSuccess;
+  hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream, p, pieces);
+  return hipGetLastError();
 }
 
 }  // namespace fa

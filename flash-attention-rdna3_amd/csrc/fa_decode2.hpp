@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
   const int b = bhk / a.heads_kv, hk = bhk - b * a.heads_kv;
 
   int len = a.max_len;
-  if (a.lens) len = min(max(a.lens[b * a.lens_stride], 0), a.max_len);
+  if (a.lens) len = min(max(a.lens[b * a.lens_stride] + a.lens_add, 0), a.max_len);
   const int nch = (len + C::CK - 1) / C::CK;
   const int per = nch / a.num_splits, extra = nch % a.num_splits;
   const int c0 = split * per + min(split, extra);
@@ -109,6 +109,8 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
   const int gq = rvalid ? r / a.seqlen_q : 0;
   const int mq = rvalid ? r - gq * a.seqlen_q : 0;
   const int hq = hk * group + gq;
+  // Last key this lane's query row sees (bottom-right causal), or all.
+  const int klim = a.causal ? len - a.seqlen_q + mq : INT_MAX;
   s16x8 qop[C::NSTEP];
   {
     const S* qrow = reinterpret_cast<const S*>(a.q) + b * a.q_stride[0] + hq * a.q_stride[1] + mq * a.q_stride[2];
@@ -224,7 +226,8 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = 16 * kb + 4 * g4 + i;
-        const float x = ((vmask >> key) & 1u) ? sacc[kb][i] * a.scale_log2 : kNegInf;
+        const float x =
+            (((vmask >> key) & 1u) && c * C::CK + key <= klim) ? sacc[kb][i] * a.scale_log2 : kNegInf;
         sacc[kb][i] = x;
         tmax = fmaxf(tmax, x);
       }

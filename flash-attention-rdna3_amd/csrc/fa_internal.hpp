@@ -23,6 +23,7 @@ hipError_t launch_bwd(const fa_bwd_params& p, int phases, hipStream_t stream);
 hipError_t launch_decode(const fa_decode_params& p, hipStream_t stream);
 hipError_t launch_paged(const fa_paged_params& p, hipStream_t stream);
 hipError_t launch_tiny(const fa_tiny_params& p, hipStream_t stream);
+hipError_t launch_append(const fa_append_params& p, hipStream_t stream);
 
 size_t decode_workspace_bytes(int batch, int heads_q, int seqlen_q, int head_dim, int num_splits);
 

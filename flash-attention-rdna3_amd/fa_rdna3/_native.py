@@ -13,7 +13,7 @@ import threading
 
 import torch
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_CODE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
 _LIB_NAME = "libfa_mi355x.so"
@@ -66,6 +66,21 @@ class DecodeParams(ctypes.Structure):
         ("cache_seqlens", ctypes.c_void_p), ("cache_seqlens_stride", ctypes.c_int64),
         ("softmax_scale", ctypes.c_float), ("num_splits", ctypes.c_int32),
         ("workspace", ctypes.c_void_p),
+        ("causal", ctypes.c_int32), ("cache_seqlens_add", ctypes.c_int32),
+    ]
+
+
+class AppendParams(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32), ("dtype", ctypes.c_int32),
+        ("k_new", ctypes.c_void_p), ("v_new", ctypes.c_void_p),
+        ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
+        ("cache_seqlens", ctypes.c_void_p), ("cache_seqlens_stride", ctypes.c_int64),
+        ("k_new_stride", _i64_4), ("v_new_stride", _i64_4),
+        ("k_cache_stride", _i64_4), ("v_cache_stride", _i64_4),
+        ("batch", ctypes.c_int32), ("heads_kv", ctypes.c_int32),
+        ("seqlen_new", ctypes.c_int32), ("seqlen_cache", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("reserved0", ctypes.c_int32),
     ]
 
 
@@ -96,10 +111,11 @@ class TinyParams(ctypes.Structure):
     ]
 
 
-_STRUCTS = (FwdParams, BwdParams, DecodeParams, PagedParams, TinyParams)
+_STRUCTS = (FwdParams, BwdParams, DecodeParams, PagedParams, TinyParams, AppendParams)
 EXPORTS = (
     "fa_abi_version", "fa_last_error_string", "fa_params_size", "fa_decode_workspace_bytes",
     "fa_fwd", "fa_bwd", "fa_bwd_phase", "fa_decode_splitk", "fa_decode_paged", "fa_tiny_fwd_f32",
+    "fa_kvcache_append",
 )
 
 _lib = None
@@ -132,7 +148,7 @@ def lib():
         handle.fa_decode_workspace_bytes.argtypes = [ctypes.c_int] * 5
         for name, struct in (("fa_fwd", FwdParams), ("fa_bwd", BwdParams),
                              ("fa_decode_splitk", DecodeParams), ("fa_decode_paged", PagedParams),
-                             ("fa_tiny_fwd_f32", TinyParams)):
+                             ("fa_tiny_fwd_f32", TinyParams), ("fa_kvcache_append", AppendParams)):
             fn = getattr(handle, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]

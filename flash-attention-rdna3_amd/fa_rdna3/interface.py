@@ -503,7 +503,14 @@ def flash_attention_decode(query, key, value, softmax_scale=None, *, cache_seqle
                 or cache_seqlens.device != query.device or cache_seqlens.shape != (batch,)):
             raise ValueError(f"cache_seqlens must be an int32 tensor of shape ({batch},) on {query.device}")
     softmax_scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
+    return _decode_launch(query, key, value, softmax_scale, cache_seqlens, causal=False)
 
+
+def _decode_launch(query, key, value, softmax_scale, lens, causal, lens_add=0):
+    """Split-K decode launch shared by flash_attention_decode and
+    flash_attention_with_kvcache (arguments already validated)."""
+    batch, heads, seqlen_q, head_dim = query.shape
+    seqlen_k = key.shape[2]
     kdim = _kernel_head_dim(head_dim)
     q, k, v = _prep(_pad_head_dim(query, kdim), _pad_head_dim(key, kdim), _pad_head_dim(value, kdim))
     if kdim <= 128:
@@ -524,14 +531,89 @@ def flash_attention_decode(query, key, value, softmax_scale=None, *, cache_seqle
         _set(getattr(p, name), _native.strides(t))
     p.batch, p.heads_q, p.seqlen_q, p.head_dim = batch, heads, seqlen_q, kdim
     p.heads_kv, p.seqlen_k = key.shape[1], seqlen_k
-    if cache_seqlens is not None:
-        p.cache_seqlens = cache_seqlens.data_ptr()
-        p.cache_seqlens_stride = cache_seqlens.stride(0)
+    if lens is not None:
+        p.cache_seqlens = lens.data_ptr()
+        p.cache_seqlens_stride = lens.stride(0)
     p.softmax_scale = softmax_scale
     p.num_splits = num_splits
     p.workspace = workspace.data_ptr()
+    p.causal = 1 if causal else 0
+    p.cache_seqlens_add = int(lens_add)
     _native.call("fa_decode_splitk", p, query)
     return out[..., :head_dim] if kdim != head_dim else out
+
+
+def _rows_vector_ready(t):
+    """True when ``t``'s rows can be written in place with 16-byte stores."""
+    esize = t.element_size()
+    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+            and all((st * esize) % 16 == 0 for st, n in zip(t.stride()[:-1], t.shape[:-1]) if n > 1))
+
+
+def flash_attention_with_kvcache(query, k_cache, v_cache, key=None, value=None, *, cache_seqlens=None,
+                                 softmax_scale=None, causal=False):
+    """Attention of new query rows against a contiguous KV cache, with an
+    optional in-place append of new keys / values (the
+    ``flash_attn_with_kvcache`` pattern; the reference's decode has no cache
+    update, interface.py:427-479).
+
+    ``query`` ``(B, Hq, Sq, D)``; ``k_cache``, ``v_cache`` ``(B, Hkv, Sc, D)``.
+    When ``key`` and ``value`` ``(B, Hkv, Snew, D)`` are given they are written
+    into the caches at rows ``[cache_seqlens[b], cache_seqlens[b] + Snew)``
+    first (rows at or past ``Sc`` are dropped); ``cache_seqlens`` (int32
+    ``(B,)``, required with ``key``) is not modified.  Sequence ``b`` then
+    attends its first ``cache_seqlens[b] + Snew`` cache rows (all ``Sc`` rows
+    when ``cache_seqlens`` is None).  ``causal`` aligns the mask bottom-right
+    per sequence: query row ``i`` sees keys ``j <= len_b - Sq + i``; a row that
+    sees no key returns zeros.  Inference-only.
+    """
+    validate_dense_inputs(query, k_cache, v_cache, dtypes=LOW_PRECISION_DTYPES)
+    validate_inference_only(query, k_cache, v_cache)
+    validate_softmax_scale(softmax_scale)
+    batch, heads, seqlen_q, head_dim = query.shape
+    heads_kv, seqlen_cache = k_cache.shape[1], k_cache.shape[2]
+    if head_dim not in _SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim {head_dim} not supported; expected one of {_SUPPORTED_HEAD_DIMS}")
+    if cache_seqlens is not None:
+        if (not isinstance(cache_seqlens, torch.Tensor) or cache_seqlens.dtype != torch.int32
+                or cache_seqlens.device != query.device or cache_seqlens.shape != (batch,)):
+            raise ValueError(f"cache_seqlens must be an int32 tensor of shape ({batch},) on {query.device}")
+    if (key is None) != (value is None):
+        raise ValueError("key and value must be given together")
+    lens = cache_seqlens
+    if key is not None:
+        if cache_seqlens is None:
+            raise ValueError("cache_seqlens is required to append key / value to the cache")
+        for name, t in (("key", key), ("value", value)):
+            if not isinstance(t, torch.Tensor) or t.dim() != 4:
+                raise ValueError(f"{name} must be a 4-D tensor (batch, heads_kv, seqlen_new, head_dim)")
+            if t.dtype != query.dtype or t.device != query.device:
+                raise ValueError(f"{name} must match query's dtype and device")
+        if key.shape != value.shape or key.shape[0] != batch or key.shape[1] != heads_kv or key.shape[3] != head_dim:
+            raise ValueError(f"key and value must have shape ({batch}, {heads_kv}, seqlen_new, {head_dim}); "
+                             f"got {tuple(key.shape)} and {tuple(value.shape)}")
+        for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+            if not _rows_vector_ready(t):
+                raise ValueError(f"{name} must have a unit last stride and 16-byte aligned rows "
+                                 "to be updated in place")
+        seqlen_new = key.shape[2]
+        if seqlen_new > 0:
+            kn, vn = _native.kernel_ready(key), _native.kernel_ready(value)
+            p = _native.AppendParams()
+            p.abi_version = ABI_VERSION
+            p.dtype = DTYPE_CODE[query.dtype]
+            p.k_new, p.v_new = kn.data_ptr(), vn.data_ptr()
+            p.k_cache, p.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+            p.cache_seqlens, p.cache_seqlens_stride = cache_seqlens.data_ptr(), cache_seqlens.stride(0)
+            for name, t in (("k_new_stride", kn), ("v_new_stride", vn), ("k_cache_stride", k_cache),
+                            ("v_cache_stride", v_cache)):
+                _set(getattr(p, name), _native.strides(t))
+            p.batch, p.heads_kv, p.seqlen_new = batch, heads_kv, seqlen_new
+            p.seqlen_cache, p.head_dim = seqlen_cache, head_dim
+            _native.call("fa_kvcache_append", p, query)
+    softmax_scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
+    return _decode_launch(query, k_cache, v_cache, softmax_scale, lens, causal=bool(causal),
+                          lens_add=0 if key is None else key.shape[2])
 
 
 # ---------------------------------------------------------------------------

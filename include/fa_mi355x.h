@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 typedef enum fa_dtype {
   FA_DTYPE_F16 = 0,
@@ -128,9 +128,14 @@ typedef struct fa_bwd_params {
  *
  * Replaces `flash_attention_decode`'s two launches (interface.py:427-479,
  * `_attention_split` at :458 and `_attention_combine` at :471).
- * q (B,Hq,Sq,D), k/v (B,Hkv,Sk,D), out like q.  Non-causal.  When
- * cache_seqlens != NULL, sequence b only attends keys [0, cache_seqlens[b])
- * (clamped to [0, Sk]); a length of 0 yields a zero output row.
+ * q (B,Hq,Sq,D), k/v (B,Hkv,Sk,D), out like q.  Non-causal as in the
+ * reference.  When cache_seqlens != NULL, sequence b only attends keys
+ * [0, len_b) with len_b = cache_seqlens[b] + cache_seqlens_add clamped to
+ * [0, Sk]; a length of 0
+ * yields a zero output row.  `causal` (no counterpart in the reference's
+ * decode; used by the kv-cache entry point below) masks bottom-right per
+ * sequence: query row i sees keys j <= len_b - Sq + i, and a row that sees
+ * no key yields zeros.
  * `workspace` must hold fa_decode_workspace_bytes(...) bytes.
  */
 typedef struct fa_decode_params {
@@ -155,7 +160,42 @@ typedef struct fa_decode_params {
   float softmax_scale;
   int32_t num_splits; /* 1..64 */
   void* workspace;
+  int32_t causal; /* 0 or 1, see above */
+  int32_t cache_seqlens_add; /* added to every cache_seqlens[b] before clamping
+                                (rows just appended by fa_kvcache_append); 0 otherwise */
 } fa_decode_params;
+
+/*
+ * Appends new keys / values to a contiguous KV cache in place:
+ * k_cache[b, h, cache_seqlens[b] + s, :] = k_new[b, h, s, :] (same for v) for
+ * s < Snew.  Rows that would land outside [0, Sc) are skipped.
+ *
+ * No counterpart in the reference (its decode takes a ready cache,
+ * interface.py:427-479); it is the cache-update half of the
+ * flash_attn_with_kvcache-style entry point (`flash_attention_with_kvcache`).
+ * k_new/v_new (B,Hkv,Snew,D); k_cache/v_cache (B,Hkv,Sc,D); cache_seqlens
+ * (B,) int32, not modified.  Unit last stride and 16-byte aligned rows.
+ */
+typedef struct fa_append_params {
+  int32_t abi_version;
+  int32_t dtype; /* FA_DTYPE_F16 or FA_DTYPE_BF16 */
+  const void* k_new;
+  const void* v_new;
+  void* k_cache;
+  void* v_cache;
+  const int32_t* cache_seqlens;
+  int64_t cache_seqlens_stride;
+  int64_t k_new_stride[4];
+  int64_t v_new_stride[4];
+  int64_t k_cache_stride[4];
+  int64_t v_cache_stride[4];
+  int32_t batch;
+  int32_t heads_kv;
+  int32_t seqlen_new;
+  int32_t seqlen_cache;
+  int32_t head_dim;
+  int32_t reserved0;
+} fa_append_params;
 
 /*
  * Paged-KV decode walking a block table (vLLM-style cache).
@@ -225,7 +265,8 @@ int fa_abi_version(void);
 const char* fa_last_error_string(void);
 
 /* sizeof() of each params struct as compiled into the library, so a binding
- * can verify its own layout: which = 0 fwd, 1 bwd, 2 decode, 3 paged, 4 tiny. */
+ * can verify its own layout: which = 0 fwd, 1 bwd, 2 decode, 3 paged, 4 tiny,
+ * 5 append. */
 size_t fa_params_size(int which);
 
 /* Bytes of scratch the split-K and paged decode need for `num_splits`. */
@@ -242,6 +283,7 @@ int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream);
 int fa_decode_splitk(const fa_decode_params* params, void* stream);
 int fa_decode_paged(const fa_paged_params* params, void* stream);
 int fa_tiny_fwd_f32(const fa_tiny_params* params, void* stream);
+int fa_kvcache_append(const fa_append_params* params, void* stream);
 
 #ifdef __cplusplus
 }

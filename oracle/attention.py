@@ -21,6 +21,13 @@ Each function names the reference code it restates
   to the tensor (varlen.py:21-27).
 * ``decode`` - kernels/decode.py:9-125 (non-causal attention of a few query
   rows over a cache), plus the ``cache_seqlens`` key limit of this build.
+* ``kvcache_attention`` - no counterpart in the reference (the SURVEY's
+  first "next" row, the flash_attn_with_kvcache pattern of FlashAttention-2):
+  new rows written into a copy of the cache at [len_b, len_b + Snew) below
+  the cache size, then ``attention_forward`` of each sequence over its first
+  len_b + Snew rows (bottom-right causal when asked).  Pinned by reduction to
+  ``decode`` (no new rows, non-causal) and to ``attention_forward`` (full
+  cache, causal), each checked against its own vectors.
 * ``paged_decode`` - kernels/paged.py:16-89: block-table gather, context
   clamped to table capacity, invalid physical ids contribute nothing.
 * ``decode_num_splits`` / ``paged_num_splits`` / ``alibi_slopes`` -
@@ -208,6 +215,30 @@ def decode(q, k, v, scale=None, cache_seqlens=None):
             continue
         out[b] = attention_forward(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n], scale=scale)[0][0]
     return out
+
+
+def kvcache_attention(q, k_cache, v_cache, k_new=None, v_new=None, cache_seqlens=None, causal=False,
+                      scale=None):
+    """q (B,Hq,Sq,D); caches (B,Hkv,Sc,D); k_new/v_new (B,Hkv,Snew,D) or None;
+    cache_seqlens (B,) or None.  Returns (out, k_cache', v_cache')."""
+    q, kc, vc = _f64(q), _f64(k_cache).copy(), _f64(v_cache).copy()
+    B, Sc = q.shape[0], kc.shape[2]
+    snew = 0 if k_new is None else k_new.shape[2]
+    base = np.full(B, Sc) if cache_seqlens is None else np.asarray(cache_seqlens, dtype=np.int64)
+    for b in range(B):
+        for s in range(snew):
+            pos = int(base[b]) + s
+            if 0 <= pos < Sc:
+                kc[b, :, pos] = _f64(k_new)[b, :, s]
+                vc[b, :, pos] = _f64(v_new)[b, :, s]
+    out = np.zeros(q.shape[:3] + (vc.shape[-1],))
+    for b in range(B):
+        n = min(max(int(base[b]) + snew, 0), Sc)
+        if n == 0:
+            continue
+        out[b] = attention_forward(q[b:b + 1], kc[b:b + 1, :, :n], vc[b:b + 1, :, :n], causal=causal,
+                                   scale=scale)[0][0]
+    return out, kc, vc
 
 
 def paged_decode(q, k_cache, v_cache, block_table, context_lens, scale=None):

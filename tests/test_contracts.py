@@ -14,7 +14,7 @@ import torch.nn.functional as F
 
 import fa_rdna3._validation as validation
 from fa_rdna3 import (alibi_slopes, flash_attention, flash_attention_decode, flash_attention_decode_paged,
-                      flash_attention_varlen, sdpa)
+                      flash_attention_varlen, flash_attention_with_kvcache, sdpa)
 from fa_rdna3.interface import _decode_num_splits, _paged_num_splits
 from fa_rdna3.sdpa import disable_rdna3_flash_attention, enable_rdna3_flash_attention, use_rdna3_flash_attention
 from oracle import attention as oracle
@@ -88,6 +88,51 @@ def test_decode_cache_seqlens_contract(monkeypatch):
     monkeypatch.setattr(validation, "_require_platform", lambda d: None)
     with pytest.raises(ValueError, match="cache_seqlens"):
         flash_attention_decode(*_dense(), cache_seqlens=torch.zeros(2, dtype=torch.int32))
+
+
+def test_kvcache_contracts(monkeypatch):
+    monkeypatch.setattr(validation, "_require_platform", lambda d: None)
+    q = torch.randn(2, 4, 3, 64, dtype=torch.float16)
+    kc = torch.randn(2, 2, 32, 64, dtype=torch.float16)
+    vc = torch.randn_like(kc)
+    kn = torch.randn(2, 2, 3, 64, dtype=torch.float16)
+    lens = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="together"):
+        flash_attention_with_kvcache(q, kc, vc, kn, None, cache_seqlens=lens)
+    with pytest.raises(ValueError, match="cache_seqlens is required"):
+        flash_attention_with_kvcache(q, kc, vc, kn, kn.clone())
+    with pytest.raises(ValueError, match="must have shape"):
+        flash_attention_with_kvcache(q, kc, vc, kn[:, :1], kn[:, :1], cache_seqlens=lens)
+    with pytest.raises(ValueError, match="dtype and device"):
+        flash_attention_with_kvcache(q, kc, vc, kn.float(), kn.float(), cache_seqlens=lens)
+    with pytest.raises(ValueError, match="in place"):
+        kc_t = torch.randn(2, 2, 64, 32, dtype=torch.float16).transpose(2, 3)  # non-unit last stride
+        flash_attention_with_kvcache(q, kc_t, vc, kn, kn.clone(), cache_seqlens=lens)
+    with pytest.raises(ValueError, match="cache_seqlens"):
+        flash_attention_with_kvcache(q, kc, vc, cache_seqlens=lens.long())
+
+
+def test_kvcache_oracle_reduces_to_decode_and_forward():
+    # The cache-update oracle is pinned by its two reductions: no new rows and
+    # no mask is `decode`; a full cache with the causal mask is the forward.
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((2, 4, 3, 16))
+    kc = rng.standard_normal((2, 2, 20, 16))
+    vc = rng.standard_normal((2, 2, 20, 16))
+    lens = np.array([7, 20])
+    out, k2, v2 = oracle.kvcache_attention(q, kc, vc, cache_seqlens=lens)
+    np.testing.assert_allclose(out, oracle.decode(q, kc, vc, cache_seqlens=lens), atol=1e-12)
+    np.testing.assert_array_equal(k2, kc)
+    out, _, _ = oracle.kvcache_attention(q, kc, vc, causal=True)
+    np.testing.assert_allclose(out, oracle.attention_forward(q, kc, vc, causal=True)[0], atol=1e-12)
+    kn = rng.standard_normal((2, 2, 3, 16))
+    vn = rng.standard_normal((2, 2, 3, 16))
+    out, k2, v2 = oracle.kvcache_attention(q, kc, vc, kn, vn, cache_seqlens=np.array([5, 18]), causal=True)
+    np.testing.assert_array_equal(k2[0, :, 5:8], kn[0])
+    np.testing.assert_array_equal(k2[1, :, 18:20], kn[1, :, :2])  # the row past the cache is dropped
+    np.testing.assert_array_equal(v2[0, :, :5], vc[0, :, :5])
+    ref0 = oracle.attention_forward(q[:1], k2[:1, :, :8], v2[:1, :, :8], causal=True)[0]
+    np.testing.assert_allclose(out[:1], ref0, atol=1e-12)
 
 
 def test_varlen_metadata_contracts(monkeypatch):
