@@ -201,7 +201,8 @@ def dkdv_roofline(tensors, iters=50):
 
 
 def run_decode_configs(iters=50):
-    from fa_rdna3 import flash_attention_decode, flash_attention_decode_paged, flash_attention_with_kvcache
+    from fa_rdna3 import (flash_attention_decode, flash_attention_decode_paged, flash_attention_decode_paged_multi,
+                          flash_attention_with_kvcache)
 
     res = {}
     stream = torch.cuda.current_stream()
@@ -251,6 +252,21 @@ def run_decode_configs(iters=50):
         gb = cfg4_bytes() / (ms * 1e-3) / 1e9
         res["cfg4_paged_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
                                     "frac_hbm": round(gb / PEAK_HBM_GBS, 4), "caches_flushed": "read of 512 MiB"}
+        # Several query rows per sequence over the cfg4 cache (speculative /
+        # chunked decode): 4 rows, bottom-right causal.
+        q4 = torch.randn(4, 32, 4, 128, generator=_gen(2)).half().cuda()
+        fm = lambda: flash_attention_decode_paged_multi(q4, kc, vc, bt, ctx, causal=True, max_context_len=16384)
+        for _ in range(5):
+            fm()
+        tot = 0.0
+        for _ in range(iters):
+            _flush(flush)
+            tot += _event_time(fm, 1, stream)
+        ms = tot / iters
+        gb = (cfg4_bytes() + 2 * 4 * 32 * 3 * 128 * 2) / (ms * 1e-3) / 1e9
+        res["paged_multi_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
+                                     "frac_hbm": round(gb / PEAK_HBM_GBS, 4), "caches_flushed": "read of 512 MiB",
+                                     "shape": "cfg4 cache, Sq = 4, causal"}
     return res
 
 

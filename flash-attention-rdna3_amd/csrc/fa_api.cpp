@@ -173,8 +173,10 @@ int fa_decode_paged(const fa_paged_params* params, void* stream) {
       p.max_blocks <= 0 || p.block_size <= 0 || p.block_size > 256 || (p.block_size & (p.block_size - 1)))
     return fail(FA_ERR_INVALID, "fa_decode_paged: bad shape");
   if (p.num_splits < 1 || p.num_splits > 64) return fail(FA_ERR_INVALID, "fa_decode_paged: num_splits");
-  if (!rows_ok(p.q, p.q_stride, 3, 2) || !rows_ok(p.k_cache, p.k_stride, 4, 2) ||
-      !rows_ok(p.v_cache, p.v_stride, 4, 2) || !rows_ok(p.out, p.out_stride, 3, 2))
+  if (p.seqlen_q < 1) return fail(FA_ERR_INVALID, "fa_decode_paged: seqlen_q must be >= 1");
+  if (p.causal != 0 && p.causal != 1) return fail(FA_ERR_INVALID, "fa_decode_paged: causal must be 0 or 1");
+  if (!rows_ok(p.q, p.q_stride, 4, 2) || !rows_ok(p.k_cache, p.k_stride, 4, 2) ||
+      !rows_ok(p.v_cache, p.v_stride, 4, 2) || !rows_ok(p.out, p.out_stride, 4, 2))
     return fail(FA_ERR_INVALID, "fa_decode_paged: q/caches/out need a unit last stride and 16-byte aligned rows");
   if (!p.block_table || !p.context_lens) return fail(FA_ERR_INVALID, "fa_decode_paged: metadata is NULL");
   if (!p.workspace || !aligned16(p.workspace)) return fail(FA_ERR_INVALID, "fa_decode_paged: workspace");

@@ -400,15 +400,8 @@ hipError_t launch_decode(const fa_decode_params& p, hipStream_t s) {
 hipError_t launch_paged(const fa_paged_params& p, hipStream_t s) {
   DecodeArgs a{};
   a.q = p.q;
-  a.q_stride[0] = p.q_stride[0];
-  a.q_stride[1] = p.q_stride[1];
-  a.q_stride[2] = 0;
-  a.q_stride[3] = p.q_stride[2];
+  for (int i = 0; i < 4; ++i) { a.q_stride[i] = p.q_stride[i]; a.out_stride[i] = p.out_stride[i]; }
   a.out = p.out;
-  a.out_stride[0] = p.out_stride[0];
-  a.out_stride[1] = p.out_stride[1];
-  a.out_stride[2] = 0;
-  a.out_stride[3] = p.out_stride[2];
   a.k = p.k_cache;
   a.v = p.v_cache;
   for (int i = 0; i < 3; ++i) { a.k_stride[i] = p.k_stride[i]; a.v_stride[i] = p.v_stride[i]; }
@@ -425,10 +418,11 @@ hipError_t launch_paged(const fa_paged_params& p, hipStream_t s) {
   a.batch = p.batch;
   a.heads_q = p.heads_q;
   a.heads_kv = p.heads_kv;
-  a.seqlen_q = 1;
+  a.seqlen_q = p.seqlen_q;
   a.head_dim = p.head_dim;
   a.scale_log2 = p.softmax_scale * kLog2e;
   a.num_splits = p.num_splits;
+  a.causal = p.causal ? 1 : 0;
   split_workspace(a, p.workspace);
   return decode_dispatch<true>(p.dtype, a, s);
 }

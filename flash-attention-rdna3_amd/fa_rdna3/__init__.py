@@ -10,6 +10,7 @@ from .interface import (
     flash_attention_decode,
     flash_attention_varlen,
     flash_attention_decode_paged,
+    flash_attention_decode_paged_multi,
     flash_attention_with_kvcache,
     alibi_slopes,
 )
@@ -24,6 +25,7 @@ __all__ = [
     "flash_attention_decode",
     "flash_attention_varlen",
     "flash_attention_decode_paged",
+    "flash_attention_decode_paged_multi",
     "flash_attention_with_kvcache",
     "alibi_slopes",
     "is_available",

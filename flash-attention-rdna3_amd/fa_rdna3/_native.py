@@ -89,13 +89,14 @@ class PagedParams(ctypes.Structure):
         ("abi_version", ctypes.c_int32), ("dtype", ctypes.c_int32),
         ("q", ctypes.c_void_p), ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p),
         ("out", ctypes.c_void_p), ("block_table", ctypes.c_void_p), ("context_lens", ctypes.c_void_p),
-        ("q_stride", _i64_3), ("k_stride", _i64_4), ("v_stride", _i64_4), ("out_stride", _i64_3),
+        ("q_stride", _i64_4), ("k_stride", _i64_4), ("v_stride", _i64_4), ("out_stride", _i64_4),
         ("block_table_stride", _i64_2), ("context_lens_stride", ctypes.c_int64),
         ("batch", ctypes.c_int32), ("heads_q", ctypes.c_int32), ("heads_kv", ctypes.c_int32),
         ("head_dim", ctypes.c_int32), ("num_blocks", ctypes.c_int32), ("block_size", ctypes.c_int32),
         ("max_blocks", ctypes.c_int32), ("num_splits", ctypes.c_int32),
-        ("softmax_scale", ctypes.c_float), ("reserved0", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float), ("seqlen_q", ctypes.c_int32),
         ("workspace", ctypes.c_void_p),
+        ("causal", ctypes.c_int32), ("reserved0", ctypes.c_int32),
     ]
 
 

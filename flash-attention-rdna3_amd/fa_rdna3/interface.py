@@ -740,6 +740,13 @@ def flash_attention_decode_paged(query, k_cache, v_cache, block_table, context_l
     validate_paged_inputs(query, k_cache, v_cache, block_table, context_lens)
     validate_inference_only(query, k_cache, v_cache)
     validate_softmax_scale(softmax_scale)
+    _paged_options(max_context_len, num_splits)
+    out = _paged_launch(query.unsqueeze(2), k_cache, v_cache, block_table, context_lens, softmax_scale,
+                        max_context_len, num_splits, causal=False)
+    return out.squeeze(2)
+
+
+def _paged_options(max_context_len, num_splits):
     if (max_context_len is not None
             and (isinstance(max_context_len, bool) or not isinstance(max_context_len, Integral)
                  or max_context_len < 0)):
@@ -748,9 +755,15 @@ def flash_attention_decode_paged(query, k_cache, v_cache, block_table, context_l
             and (isinstance(num_splits, bool) or not isinstance(num_splits, Integral)
                  or not 1 <= num_splits <= 32)):
         raise ValueError("num_splits must be an integer between 1 and 32 or None")
+
+
+def _paged_launch(query, k_cache, v_cache, block_table, context_lens, softmax_scale, max_context_len,
+                  num_splits, causal):
+    """Paged decode launch for a (batch, q_heads, Sq, head_dim) query (arguments
+    already validated)."""
     max_context_len = None if max_context_len is None else int(max_context_len)
     num_splits = None if num_splits is None else int(num_splits)
-    batch, q_heads, head_dim = query.shape
+    batch, q_heads, seqlen_q, head_dim = query.shape
     num_blocks, block_size, kv_heads = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
     softmax_scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
 
@@ -759,15 +772,15 @@ def flash_attention_decode_paged(query, k_cache, v_cache, block_table, context_l
         max_keys = block_table.shape[1] * block_size
         if max_context_len is not None:
             max_keys = min(max_keys, max_context_len)
-        splits = _streaming_decode_splits(batch, kv_heads, q_heads // kv_heads, max_keys,
+        splits = _streaming_decode_splits(batch, kv_heads, (q_heads // kv_heads) * seqlen_q, max_keys,
                                           _cu_count(query.device))
     else:
         splits = int(_paged_num_splits(batch, q_heads, block_size, block_table.shape[1],
                                        2 * _cu_count(query.device), max_context_len=max_context_len,
                                        requested_splits=num_splits))
     q, kc, vc = _prep(_pad_head_dim(query, kdim), _pad_head_dim(k_cache, kdim), _pad_head_dim(v_cache, kdim))
-    out = torch.empty((batch, q_heads, kdim), dtype=query.dtype, device=query.device)
-    workspace = torch.empty(_native.decode_workspace_bytes(batch, q_heads, 1, kdim, splits),
+    out = torch.empty((batch, q_heads, seqlen_q, kdim), dtype=query.dtype, device=query.device)
+    workspace = torch.empty(_native.decode_workspace_bytes(batch, q_heads, seqlen_q, kdim, splits),
                             dtype=torch.uint8, device=query.device)
     p = _native.PagedParams()
     p.abi_version = ABI_VERSION
@@ -784,6 +797,34 @@ def flash_attention_decode_paged(query, k_cache, v_cache, block_table, context_l
     p.num_blocks, p.block_size, p.max_blocks = num_blocks, block_size, block_table.shape[1]
     p.num_splits = splits
     p.softmax_scale = softmax_scale
+    p.seqlen_q = seqlen_q
+    p.causal = 1 if causal else 0
     p.workspace = workspace.data_ptr()
     _native.call("fa_decode_paged", p, query)
     return out[..., :head_dim] if kdim != head_dim else out
+
+
+def flash_attention_decode_paged_multi(query, k_cache, v_cache, block_table, context_lens, softmax_scale=None,
+                                       *, causal=True, max_context_len=None, num_splits=None):
+    """Paged decode of several query rows per sequence (speculative or chunked
+    decode over a vLLM-style cache; no counterpart in the reference, whose
+    paged decode takes one row, interface.py:643-728).
+
+    ``query`` ``(batch, q_heads, Sq, head_dim)``; the other arguments as in
+    :func:`flash_attention_decode_paged`, with ``context_lens`` counting the
+    query rows' own keys (already written to their pages).  ``causal`` aligns
+    bottom-right per sequence: row ``i`` sees keys ``j <= context_len - Sq + i``.
+    Returns ``(batch, q_heads, Sq, head_dim)``.  Inference-only.
+    """
+    _require_4d_query(query)
+    validate_paged_inputs(query.select(2, 0), k_cache, v_cache, block_table, context_lens)
+    validate_inference_only(query, k_cache, v_cache)
+    validate_softmax_scale(softmax_scale)
+    _paged_options(max_context_len, num_splits)
+    return _paged_launch(query, k_cache, v_cache, block_table, context_lens, softmax_scale, max_context_len,
+                         num_splits, causal=bool(causal))
+
+
+def _require_4d_query(query):
+    if not isinstance(query, torch.Tensor) or query.dim() != 4 or query.shape[2] < 1:
+        raise ValueError("query must be (batch, heads, seqlen_q, dim) with seqlen_q >= 1")

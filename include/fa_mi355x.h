@@ -202,10 +202,14 @@ typedef struct fa_append_params {
  *
  * Replaces `flash_attention_decode_paged`'s launches (interface.py:643-728,
  * `_attention_decode_paged` at :704 and `_attention_combine` at :720).
- * q (B,Hq,D); k_cache/v_cache (num_blocks, block_size, Hkv, D);
+ * q (B,Hq,D) in the reference, here (B,Hq,Sq,D) with seqlen_q = Sq (1 for
+ * the reference's case); k_cache/v_cache (num_blocks, block_size, Hkv, D);
  * block_table (B, max_blocks) int32; context_lens (B,) int32.  Context is
  * clamped to [0, max_blocks*block_size] and physical ids outside
  * [0, num_blocks) contribute nothing (reference paged.py:37-38, :58-59).
+ * With Sq > 1 (speculative / chunked decode, no counterpart in the
+ * reference) `causal` masks bottom-right per sequence as in
+ * fa_decode_params.
  */
 typedef struct fa_paged_params {
   int32_t abi_version;
@@ -216,10 +220,10 @@ typedef struct fa_paged_params {
   void* out;
   const int32_t* block_table;
   const int32_t* context_lens;
-  int64_t q_stride[3];  /* batch, head, dim */
+  int64_t q_stride[4];  /* batch, head, row, dim */
   int64_t k_stride[4];  /* block, position, head, dim */
   int64_t v_stride[4];
-  int64_t out_stride[3];
+  int64_t out_stride[4];
   int64_t block_table_stride[2];
   int64_t context_lens_stride;
   int32_t batch;
@@ -231,8 +235,10 @@ typedef struct fa_paged_params {
   int32_t max_blocks; /* columns of block_table */
   int32_t num_splits; /* 1..64 */
   float softmax_scale;
+  int32_t seqlen_q; /* query rows per sequence, >= 1 */
+  void* workspace; /* fa_decode_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits) */
+  int32_t causal;  /* 0 or 1 */
   int32_t reserved0;
-  void* workspace; /* fa_decode_workspace_bytes(batch, heads_q, 1, head_dim, num_splits) */
 } fa_paged_params;
 
 /*

@@ -30,6 +30,11 @@ Each function names the reference code it restates
   cache, causal), each checked against its own vectors.
 * ``paged_decode`` - kernels/paged.py:16-89: block-table gather, context
   clamped to table capacity, invalid physical ids contribute nothing.
+* ``paged_attention`` - no counterpart in the reference (the SURVEY's second
+  "next" row): ``paged_decode`` for Sq query rows per sequence, keys kept at
+  their cache positions, bottom-right causal when asked.  Pinned by its
+  reduction to ``paged_decode`` (Sq = 1) and to ``kvcache_attention`` over
+  the gathered contiguous cache.
 * ``decode_num_splits`` / ``paged_num_splits`` / ``alibi_slopes`` -
   interface.py:53-58, :61-77, :136-151.
 * ``split_combine`` - decode.py:79-125: LSE-weighted merge of split partials.
@@ -266,6 +271,38 @@ def paged_decode(q, k_cache, v_cache, block_table, context_lens, scale=None):
             s = (kk[:, h // g] @ q[b, h]) * scale
             p = np.exp(s - s.max())
             p /= p.sum()
+            out[b, h] = p @ vv[:, h // g]
+    return out
+
+
+def paged_attention(q, k_cache, v_cache, block_table, context_lens, causal=False, scale=None):
+    """q (B,Hq,Sq,D); caches (NB,P,Hkv,D); block_table (B,M); context_lens (B,).
+    Key n of sequence b is page block_table[b, n // P], row n % P; keys on
+    invalid pages contribute nothing but keep their positions."""
+    q, kc, vc = _f64(q), _f64(k_cache), _f64(v_cache)
+    bt = np.asarray(block_table, dtype=np.int64)
+    B, Hq, Sq, D = q.shape
+    NB, P, Hkv, _ = kc.shape
+    g = Hq // Hkv
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    out = np.zeros((B, Hq, Sq, vc.shape[-1]))
+    for b in range(B):
+        ctx = min(max(int(context_lens[b]), 0), bt.shape[1] * P)
+        if ctx == 0:
+            continue
+        phys = bt[b, np.arange(ctx) // P]
+        ok = (phys >= 0) & (phys < NB)
+        rows = np.arange(ctx) % P
+        kk = np.zeros((ctx, Hkv, D))
+        vv = np.zeros((ctx, Hkv, vc.shape[-1]))
+        kk[ok] = kc[phys[ok], rows[ok]]
+        vv[ok] = vc[phys[ok], rows[ok]]
+        keep = np.broadcast_to(ok[None, :], (Sq, ctx)).copy()
+        if causal:
+            keep &= np.arange(ctx)[None, :] <= np.arange(Sq)[:, None] + (ctx - Sq)
+        for h in range(Hq):
+            s = np.where(keep, (q[b, h] @ kk[:, h // g].T) * scale, NEG_INF)
+            p, _ = _softmax_rows(s)
             out[b, h] = p @ vv[:, h // g]
     return out
 

@@ -14,7 +14,8 @@ import torch.nn.functional as F
 
 import fa_rdna3._validation as validation
 from fa_rdna3 import (alibi_slopes, flash_attention, flash_attention_decode, flash_attention_decode_paged,
-                      flash_attention_varlen, flash_attention_with_kvcache, sdpa)
+                      flash_attention_decode_paged_multi, flash_attention_varlen, flash_attention_with_kvcache,
+                      sdpa)
 from fa_rdna3.interface import _decode_num_splits, _paged_num_splits
 from fa_rdna3.sdpa import disable_rdna3_flash_attention, enable_rdna3_flash_attention, use_rdna3_flash_attention
 from oracle import attention as oracle
@@ -133,6 +134,36 @@ def test_kvcache_oracle_reduces_to_decode_and_forward():
     np.testing.assert_array_equal(v2[0, :, :5], vc[0, :, :5])
     ref0 = oracle.attention_forward(q[:1], k2[:1, :, :8], v2[:1, :, :8], causal=True)[0]
     np.testing.assert_allclose(out[:1], ref0, atol=1e-12)
+
+
+def test_paged_attention_oracle_reductions():
+    # Multi-row paged oracle: one row reduces to paged_decode; with all pages
+    # valid it equals the kv-cache oracle over the gathered contiguous cache.
+    rng = np.random.default_rng(9)
+    kc = rng.standard_normal((12, 4, 2, 16))
+    vc = rng.standard_normal((12, 4, 2, 16))
+    bt = rng.permutation(12).reshape(2, 6)
+    ctx = np.array([13, 24])
+    q1 = rng.standard_normal((2, 4, 16))
+    np.testing.assert_allclose(oracle.paged_attention(q1[:, :, None], kc, vc, bt, ctx)[:, :, 0],
+                               oracle.paged_decode(q1, kc, vc, bt, ctx), atol=1e-12)
+    q = rng.standard_normal((2, 4, 5, 16))
+    gk = np.stack([kc[bt[b]].reshape(24, 2, 16).transpose(1, 0, 2) for b in range(2)])
+    gv = np.stack([vc[bt[b]].reshape(24, 2, 16).transpose(1, 0, 2) for b in range(2)])
+    ref, _, _ = oracle.kvcache_attention(q, gk, gv, cache_seqlens=ctx, causal=True)
+    np.testing.assert_allclose(oracle.paged_attention(q, kc, vc, bt, ctx, causal=True), ref, atol=1e-12)
+
+
+def test_paged_multi_contract(monkeypatch):
+    monkeypatch.setattr(validation, "_require_platform", lambda d: None)
+    q = torch.randn(2, 4, 64, dtype=torch.float16)
+    kc = torch.randn(8, 16, 2, 64, dtype=torch.float16)
+    bt = torch.zeros(2, 4, dtype=torch.int32)
+    ctx = torch.ones(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="seqlen_q"):
+        flash_attention_decode_paged_multi(q, kc, kc.clone(), bt, ctx)
+    with pytest.raises(ValueError, match="seqlen_q"):
+        flash_attention_decode_paged_multi(q[:, :, None, :][:, :, :0], kc, kc.clone(), bt, ctx)
 
 
 def test_varlen_metadata_contracts(monkeypatch):
