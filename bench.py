@@ -220,6 +220,23 @@ def run_decode_configs(iters=50):
         gb = cfg3_bytes(lens.tolist()) / (ms * 1e-3) / 1e9
         res["cfg3_splitk_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
                                      "frac_hbm": round(gb / PEAK_HBM_GBS, 4), "caches_flushed": "read of 512 MiB"}
+        # The cfg3 cache stored as fp8 (OCP e4m3, per-tensor scale 1): half
+        # the bytes of the fp16 cache.
+        k8, v8 = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
+        f8 = lambda: flash_attention_decode(q, k8, v8, cache_seqlens=lens)
+        for _ in range(5):
+            f8()
+        tot = 0.0
+        for _ in range(iters):
+            _flush(flush)
+            tot += _event_time(f8, 1, stream)
+        ms = tot / iters
+        b8 = sum(int(n) for n in lens.tolist()) * 8 * 128 * 1 * 2 + 2 * 4 * 32 * 128 * 2
+        gb = b8 / (ms * 1e-3) / 1e9
+        res["cfg3_fp8_kv_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
+                                     "frac_hbm": round(gb / PEAK_HBM_GBS, 4), "caches_flushed": "read of 512 MiB",
+                                     "bytes": b8}
+        del k8, v8
         # KV-cache entry point on the cfg3 cache: 4 new tokens per sequence
         # appended in place at the cfg3 lengths, then 4 query rows attend
         # bottom-right causally (speculative / chunked decode step).

@@ -154,7 +154,11 @@ int fa_decode_splitk(const fa_decode_params* params, void* stream) {
       p.seqlen_k <= 0)
     return fail(FA_ERR_INVALID, "fa_decode_splitk: bad shape");
   if (p.num_splits < 1 || p.num_splits > 64) return fail(FA_ERR_INVALID, "fa_decode_splitk: num_splits");
-  if (!rows_ok(p.q, p.q_stride, 4, 2) || !rows_ok(p.k, p.k_stride, 4, 2) || !rows_ok(p.v, p.v_stride, 4, 2) ||
+  if (p.kv_fp8 != 0 && p.kv_fp8 != 1) return fail(FA_ERR_INVALID, "fa_decode_splitk: kv_fp8 must be 0 or 1");
+  if (p.kv_fp8 && p.head_dim > 128)
+    return fail(FA_ERR_UNSUPPORTED, "fa_decode_splitk: fp8 caches need head_dim <= 128, got %d", p.head_dim);
+  const int kes = p.kv_fp8 ? 1 : 2;
+  if (!rows_ok(p.q, p.q_stride, 4, 2) || !rows_ok(p.k, p.k_stride, 4, kes) || !rows_ok(p.v, p.v_stride, 4, kes) ||
       !rows_ok(p.out, p.out_stride, 4, 2))
     return fail(FA_ERR_INVALID, "fa_decode_splitk: q/k/v/out need a unit last stride and 16-byte aligned rows");
   if (!p.workspace || !aligned16(p.workspace)) return fail(FA_ERR_INVALID, "fa_decode_splitk: workspace");

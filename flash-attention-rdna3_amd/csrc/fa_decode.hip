@@ -51,6 +51,8 @@ struct DecodeArgs {
   float scale_log2;
   int32_t num_splits;
   int32_t causal;       // bottom-right per sequence: row i sees keys <= len - Sq + i
+  int32_t kv8;          // contiguous fp8 (OCP e4m3) K/V, decode2 path only
+  float out_scale;      // multiplies the output (v_scale of an fp8 cache); 1 otherwise
   float* ws_o;          // [splits][B][Hq][Sq][D] fp32
   float* ws_lse;        // [splits][B][Hq][Sq] fp32
 };
@@ -323,6 +325,9 @@ static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
       const int nrb = (group * a.seqlen_q + 15) / 16;
       dim3 grid(a.num_splits, a.batch * a.heads_kv * nrb);
       auto kern = decode2_kernel<Tag, D, PAGED ? 1 : 0>;
+      if constexpr (!PAGED) {
+        if (a.kv8) kern = decode2_kernel<Tag, D, 0, true>;
+      }
       hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(kern, grid, dim3(C::NT), C::LDS_BYTES, stream, a);
@@ -333,6 +338,7 @@ static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
       return hipGetLastError();
     }
   }
+  if (a.kv8) return hipErrorInvalidValue;  // fp8 caches: contiguous, head_dim <= 128 only
   using C = DecCfg<Tag, D>;
   auto kern = decode_kernel<Tag, D, PAGED>;
   hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
@@ -390,7 +396,11 @@ hipError_t launch_decode(const fa_decode_params& p, hipStream_t s) {
   a.heads_kv = p.heads_kv;
   a.seqlen_q = p.seqlen_q;
   a.head_dim = p.head_dim;
-  a.scale_log2 = p.softmax_scale * kLog2e;
+  a.kv8 = p.kv_fp8 ? 1 : 0;
+  // An fp8 cache holds K / k_scale and V / v_scale: k_scale joins the logit
+  // scale, v_scale multiplies the output.
+  a.scale_log2 = p.softmax_scale * (a.kv8 ? p.k_scale : 1.f) * kLog2e;
+  a.out_scale = a.kv8 ? p.v_scale : 1.f;
   a.num_splits = p.num_splits;
   a.causal = p.causal ? 1 : 0;
   split_workspace(a, p.workspace);
@@ -423,6 +433,7 @@ hipError_t launch_paged(const fa_paged_params& p, hipStream_t s) {
   a.scale_log2 = p.softmax_scale * kLog2e;
   a.num_splits = p.num_splits;
   a.causal = p.causal ? 1 : 0;
+  a.out_scale = 1.f;
   split_workspace(a, p.workspace);
   return decode_dispatch<true>(p.dtype, a, s);
 }

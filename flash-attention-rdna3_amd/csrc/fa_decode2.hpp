@@ -39,7 +39,7 @@ __device__ inline void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
-template <int D>
+template <int D, bool KV8 = false>
 struct Dec2Cfg {
   static constexpr int NW = 4;
   static constexpr int NT = 64 * NW;
@@ -55,13 +55,40 @@ struct Dec2Cfg {
 #ifndef FA_DEC_SLOT_VGPRS
 #define FA_DEC_SLOT_VGPRS 128
 #endif
-  static constexpr int NBUF = FA_DEC_SLOT_VGPRS / (4 * PER);
+  // A load is 16 bytes (8 16-bit elements) or, for an fp8 cache, 8 bytes.
+  static constexpr int NBUF = FA_DEC_SLOT_VGPRS / ((KV8 ? 2 : 4) * PER);
   static constexpr int WAVE_ELEMS = TILE;            // one private V tile per wave
   static constexpr int LOOP_BYTES = NW * WAVE_ELEMS * 2;
   static constexpr int OLD = 17;                     // merge buffer row stride (floats)
   static constexpr int MERGE_BYTES = NW * D * OLD * 4 + 2 * NW * 16 * 4;
   static constexpr int LDS_BYTES = LOOP_BYTES > MERGE_BYTES ? LOOP_BYTES : MERGE_BYTES;
 };
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Eight fp8 (OCP e4m3) cache elements -> an 8-element 16-bit operand of the
+// query's type.  The conversion is exact (e4m3 values are representable in
+// fp16 and bf16); the per-tensor scales are applied outside (k_scale in the
+// logit scale, v_scale on the output).
+template <typename Tag, bool HI>
+__device__ inline uint32_t fp8x2_to_16(uint32_t w) {
+  if constexpr (std::is_same<Tag, bf16_t>::value)
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, HI));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, HI));
+}
+template <typename Tag>
+__device__ inline s16x8 fp8x8_to_op(u32x2 r) {
+  const uint32_t p[4] = {fp8x2_to_16<Tag, false>(r[0]), fp8x2_to_16<Tag, true>(r[0]),
+                         fp8x2_to_16<Tag, false>(r[1]), fp8x2_to_16<Tag, true>(r[1])};
+  s16x8 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = (short)(p[i] & 0xFFFFu);
+    o[2 * i + 1] = (short)(p[i] >> 16);
+  }
+  return o;
+}
 
 // PAGE: 0 contiguous cache; 1 paged with block_size >= 16 (a 32-key chunk
 // spans at most two pages, whose ids are wave-uniform scalar loads).
@@ -76,13 +103,17 @@ struct Dec2Cfg {
 // ordinary vector loads into registers: the compiler's per-register vmcnt
 // tracking then waits exactly for the slot being used.  (Asynchronous LDS DMA
 // in this loop makes it drain every load at the loop head instead.)
-template <typename Tag, int D, int PAGE>
+// KV8: the contiguous cache holds fp8 (OCP e4m3) K and V.
+template <typename Tag, int D, int PAGE, bool KV8 = false>
 __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
   static_assert(PAGE == 0 || PAGE == 1, "decode2 handles contiguous and >=16-key pages");
+  static_assert(!(KV8 && PAGE), "fp8 caches are contiguous");
   constexpr bool PAGED = PAGE != 0;
-  using C = Dec2Cfg<D>;
+  using C = Dec2Cfg<D, KV8>;
   using EL = Elem<Tag>;
   using S = uint16_t;
+  using KE = typename std::conditional<KV8, uint8_t, S>::type;   // cache element
+  using KRaw = typename std::conditional<KV8, u32x2, s16x8>::type;  // one load: 8 elements
   extern __shared__ __align__(16) unsigned char smem_raw[];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -124,8 +155,8 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
   }
 
   typedef __attribute__((address_space(3))) void lds_void;
-  const S* kbase = reinterpret_cast<const S*>(a.k);
-  const S* vbase = reinterpret_cast<const S*>(a.v);
+  const KE* kbase = reinterpret_cast<const KE*>(a.k);
+  const KE* vbase = reinterpret_cast<const KE*>(a.v);
   if constexpr (!PAGED) {
     kbase += b * a.k_stride[0] + hk * a.k_stride[1];
     vbase += b * a.v_stride[0] + hk * a.v_stride[1];
@@ -167,9 +198,9 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
 
   // Chunk slot j: K registers kr[j], V registers vr[j].  `live` false loads
   // the stand-in row 0 (nothing of it is used).
-  s16x8 kr[C::NBUF][2][C::NSTEP];
-  s16x8 vreg[C::NBUF][C::VLOADS];
-  auto issue_chunk = [&](int c, bool live, s16x8 (&kd)[2][C::NSTEP], s16x8 (&vd)[C::VLOADS]) {
+  KRaw kr[C::NBUF][2][C::NSTEP];
+  KRaw vreg[C::NBUF][C::VLOADS];
+  auto issue_chunk = [&](int c, bool live, KRaw (&kd)[2][C::NSTEP], KRaw (&vd)[C::VLOADS]) {
     const int n0 = c * C::CK;
     int pg0 = 0, pg1 = 0;
     if constexpr (PAGE == 1) chunk_pages(c, pg0, pg1);
@@ -178,7 +209,10 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
       int64_t ko = key_off(n0 + 16 * kb + l16, pg0, pg1, a.k_stride);
       ko = (ko < 0 || !live) ? 0 : ko;
 #pragma unroll
-      for (int s = 0; s < C::NSTEP; ++s) kd[kb][s] = load_op<Tag>(kbase + ko + 8 * (4 * s + g4));
+      for (int s = 0; s < C::NSTEP; ++s) {
+        if constexpr (KV8) kd[kb][s] = *reinterpret_cast<const u32x2*>(kbase + ko + 8 * (4 * s + g4));
+        else kd[kb][s] = load_op<Tag>(kbase + ko + 8 * (4 * s + g4));
+      }
     }
 #pragma unroll
     for (int i = 0; i < C::VLOADS; ++i) {
@@ -186,7 +220,7 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
       const int row = slot / C::CPR;
       int64_t vo = key_off(n0 + row, pg0, pg1, a.v_stride);
       vo = (vo < 0 || !live) ? 0 : vo;
-      vd[i] = *reinterpret_cast<const s16x8*>(vbase + vo + (slot % C::CPR) * 8);
+      vd[i] = *reinterpret_cast<const KRaw*>(vbase + vo + (slot % C::CPR) * 8);
     }
   };
   // Bit k of the result: key n0 + k of the chunk is visible.
@@ -204,21 +238,25 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
   for (int i = 0; i < C::NDB; ++i) acc[i] = f32x4v{0.f, 0.f, 0.f, 0.f};
 
   S* const Vs = wbase;
-  auto compute_chunk = [&](int c, const s16x8 (&kd)[2][C::NSTEP], const s16x8 (&vd)[C::VLOADS]) {
+  auto to_op = [&](const KRaw& r) -> s16x8 {
+    if constexpr (KV8) return fp8x8_to_op<Tag>(r);
+    else return r;
+  };
+  auto compute_chunk = [&](int c, const KRaw (&kd)[2][C::NSTEP], const KRaw (&vd)[C::VLOADS]) {
     const uint32_t vmask = chunk_mask(c);
     // V rows -> this wave's LDS tile (swizzled); the previous chunk's reads of
     // the tile precede these writes in the wave's LDS order.
 #pragma unroll
     for (int i = 0; i < C::VLOADS; ++i) {
       const int slot = 64 * i + lane;
-      *reinterpret_cast<s16x8*>(Vs + swz_off<D>(slot / C::CPR, (slot % C::CPR) * 8)) = vd[i];
+      *reinterpret_cast<s16x8*>(Vs + swz_off<D>(slot / C::CPR, (slot % C::CPR) * 8)) = to_op(vd[i]);
     }
     f32x4v sacc[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       sacc[kb] = f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < C::NSTEP; ++s) sacc[kb] = mma16<Tag>(kd[kb][s], qop[s], sacc[kb]);
+      for (int s = 0; s < C::NSTEP; ++s) sacc[kb] = mma16<Tag>(to_op(kd[kb][s]), qop[s], sacc[kb]);
     }
     float tmax = kNegInf;
 #pragma unroll
@@ -333,7 +371,7 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
       o += ow[(w * D + d) * C::OLD + cc] * sc;
     }
     const float Ls = (L == 0.f) ? 1.f : L;
-    o /= Ls;
+    o = o / Ls * a.out_scale;  // out_scale: v_scale of an fp8 cache, else 1
     const int gg = row / a.seqlen_q, mm = row - gg * a.seqlen_q;
     const int hh = hk * group + gg;
     if (a.num_splits == 1) {

@@ -67,6 +67,8 @@ class DecodeParams(ctypes.Structure):
         ("softmax_scale", ctypes.c_float), ("num_splits", ctypes.c_int32),
         ("workspace", ctypes.c_void_p),
         ("causal", ctypes.c_int32), ("cache_seqlens_add", ctypes.c_int32),
+        ("kv_fp8", ctypes.c_int32), ("k_scale", ctypes.c_float), ("v_scale", ctypes.c_float),
+        ("reserved0", ctypes.c_int32),
     ]
 
 

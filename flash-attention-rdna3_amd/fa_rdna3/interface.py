@@ -482,7 +482,8 @@ def flash_attention(query, key, value, causal=False, softmax_scale=None, window_
 # Split-K decode (reference interface.py:427-479)
 # ---------------------------------------------------------------------------
 
-def flash_attention_decode(query, key, value, softmax_scale=None, *, cache_seqlens=None):
+def flash_attention_decode(query, key, value, softmax_scale=None, *, cache_seqlens=None, k_scale=None,
+                           v_scale=None):
     """Split-K attention for autoregressive decode (small query, long KV).
 
     The key range is split across workgroups so a tiny query fills the GPU;
@@ -490,8 +491,19 @@ def flash_attention_decode(query, key, value, softmax_scale=None, *, cache_seqle
     inference-only.  ``cache_seqlens`` (optional int32 ``(batch,)``) limits
     sequence b to its first ``cache_seqlens[b]`` keys (an MI355X-build
     extension; absent, every key is visible as in the reference).
+
+    ``key`` / ``value`` may also be ``torch.float8_e4m3fn`` caches holding
+    K / k_scale and V / v_scale (per-tensor scales, default 1; head_dim <= 128;
+    another MI355X-build extension): they are read as fp8, half the bytes of
+    a 16-bit cache, and converted exactly to the query's type in registers.
     """
-    validate_dense_inputs(query, key, value, dtypes=LOW_PRECISION_DTYPES)
+    kv_fp8 = isinstance(key, torch.Tensor) and key.dtype == torch.float8_e4m3fn
+    if kv_fp8:
+        _validate_fp8_kv(query, key, value, k_scale, v_scale)
+    else:
+        if k_scale is not None or v_scale is not None:
+            raise ValueError("k_scale and v_scale apply to float8_e4m3fn key / value caches only")
+        validate_dense_inputs(query, key, value, dtypes=LOW_PRECISION_DTYPES)
     validate_inference_only(query, key, value)
     validate_softmax_scale(softmax_scale)
     batch, heads, seqlen_q, head_dim = query.shape
@@ -503,16 +515,43 @@ def flash_attention_decode(query, key, value, softmax_scale=None, *, cache_seqle
                 or cache_seqlens.device != query.device or cache_seqlens.shape != (batch,)):
             raise ValueError(f"cache_seqlens must be an int32 tensor of shape ({batch},) on {query.device}")
     softmax_scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
+    if kv_fp8:
+        return _decode_launch(query, key, value, softmax_scale, cache_seqlens, causal=False,
+                              fp8_scales=(1.0 if k_scale is None else float(k_scale),
+                                          1.0 if v_scale is None else float(v_scale)))
     return _decode_launch(query, key, value, softmax_scale, cache_seqlens, causal=False)
 
 
-def _decode_launch(query, key, value, softmax_scale, lens, causal, lens_add=0):
+def _validate_fp8_kv(query, key, value, k_scale, v_scale):
+    """Contracts of an fp8 (e4m3) KV cache: the dense shape rules, checked on
+    16-bit stand-ins of the same shapes, plus the fp8-specific ones."""
+    if not isinstance(value, torch.Tensor) or value.dtype != torch.float8_e4m3fn:
+        raise ValueError("key and value must both be float8_e4m3fn caches")
+    for name, sc in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if sc is not None and (isinstance(sc, bool) or not isinstance(sc, (int, float))
+                               or not math.isfinite(float(sc)) or float(sc) <= 0.0):
+            raise ValueError(f"{name} must be a positive finite number or None")
+    if not isinstance(query, torch.Tensor) or query.dtype not in LOW_PRECISION_DTYPES:
+        raise ValueError("query must be float16 or bfloat16 with an fp8 KV cache")
+    stand_in = lambda t: torch.empty_strided(t.shape, [0] * t.dim(), dtype=query.dtype, device=t.device)
+    validate_dense_inputs(query, stand_in(key), stand_in(value), dtypes=LOW_PRECISION_DTYPES)
+    if query.shape[3] not in (32, 64, 128):
+        raise ValueError(f"fp8 KV caches need head_dim 32, 64 or 128, got {query.shape[3]}")
+
+
+def _decode_launch(query, key, value, softmax_scale, lens, causal, lens_add=0, fp8_scales=None):
     """Split-K decode launch shared by flash_attention_decode and
     flash_attention_with_kvcache (arguments already validated)."""
     batch, heads, seqlen_q, head_dim = query.shape
     seqlen_k = key.shape[2]
     kdim = _kernel_head_dim(head_dim)
-    q, k, v = _prep(_pad_head_dim(query, kdim), _pad_head_dim(key, kdim), _pad_head_dim(value, kdim))
+    if fp8_scales is not None:
+        # fp8 rows: unit last stride and 16-byte aligned rows (contiguous copy
+        # otherwise); head_dim is one of the kernel's dims, so no padding.
+        q = _prep(query)[0]
+        k, v = _native.kernel_ready(key), _native.kernel_ready(value)
+    else:
+        q, k, v = _prep(_pad_head_dim(query, kdim), _pad_head_dim(key, kdim), _pad_head_dim(value, kdim))
     if kdim <= 128:
         group = heads // key.shape[1]
         num_splits = _streaming_decode_splits(batch, key.shape[1], group * seqlen_q, seqlen_k,
@@ -539,6 +578,9 @@ def _decode_launch(query, key, value, softmax_scale, lens, causal, lens_add=0):
     p.workspace = workspace.data_ptr()
     p.causal = 1 if causal else 0
     p.cache_seqlens_add = int(lens_add)
+    if fp8_scales is not None:
+        p.kv_fp8 = 1
+        p.k_scale, p.v_scale = fp8_scales
     _native.call("fa_decode_splitk", p, query)
     return out[..., :head_dim] if kdim != head_dim else out
 

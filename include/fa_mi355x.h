@@ -163,6 +163,11 @@ typedef struct fa_decode_params {
   int32_t causal; /* 0 or 1, see above */
   int32_t cache_seqlens_add; /* added to every cache_seqlens[b] before clamping
                                 (rows just appended by fa_kvcache_append); 0 otherwise */
+  int32_t kv_fp8;  /* 1: k and v are fp8 (OCP e4m3) holding K / k_scale and V / v_scale
+                      (head_dim <= 128); 0: they have `dtype` and the scales are ignored */
+  float k_scale;
+  float v_scale;
+  int32_t reserved0;
 } fa_decode_params;
 
 /*

@@ -166,6 +166,25 @@ def test_paged_multi_contract(monkeypatch):
         flash_attention_decode_paged_multi(q[:, :, None, :][:, :, :0], kc, kc.clone(), bt, ctx)
 
 
+def test_fp8_decode_contracts(monkeypatch):
+    monkeypatch.setattr(validation, "_require_platform", lambda d: None)
+    q = torch.randn(2, 4, 1, 64, dtype=torch.float16)
+    k8 = torch.randn(2, 2, 32, 64).to(torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="both be float8"):
+        flash_attention_decode(q, k8, torch.randn(2, 2, 32, 64, dtype=torch.float16))
+    with pytest.raises(ValueError, match="k_scale"):
+        flash_attention_decode(q, k8, k8.clone(), k_scale=0.0)
+    with pytest.raises(ValueError, match="fp8 KV caches need head_dim"):
+        flash_attention_decode(torch.randn(2, 4, 1, 256, dtype=torch.float16),
+                               torch.randn(2, 2, 32, 256).to(torch.float8_e4m3fn),
+                               torch.randn(2, 2, 32, 256).to(torch.float8_e4m3fn))
+    with pytest.raises(ValueError, match="float8_e4m3fn key / value caches only"):
+        flash_attention_decode(q, torch.randn(2, 2, 32, 64, dtype=torch.float16),
+                               torch.randn(2, 2, 32, 64, dtype=torch.float16), v_scale=2.0)
+    with pytest.raises(ValueError, match="same batch size"):
+        flash_attention_decode(q, k8[:1], k8[:1].clone())
+
+
 def test_varlen_metadata_contracts(monkeypatch):
     monkeypatch.setattr(validation, "_require_platform", lambda d: None)
     q = torch.randn(8, 4, 64, dtype=torch.float16)
