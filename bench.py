@@ -269,6 +269,22 @@ def run_decode_configs(iters=50):
         gb = cfg4_bytes() / (ms * 1e-3) / 1e9
         res["cfg4_paged_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
                                     "frac_hbm": round(gb / PEAK_HBM_GBS, 4), "caches_flushed": "read of 512 MiB"}
+        # The cfg4 cache stored as fp8 (OCP e4m3, scale 1).
+        kc8, vc8 = kc.to(torch.float8_e4m3fn), vc.to(torch.float8_e4m3fn)
+        f48 = lambda: flash_attention_decode_paged(q, kc8, vc8, bt, ctx, max_context_len=16384)
+        for _ in range(5):
+            f48()
+        tot = 0.0
+        for _ in range(iters):
+            _flush(flush)
+            tot += _event_time(f48, 1, stream)
+        ms = tot / iters
+        b8 = 4 * 16384 * 8 * 128 * 1 * 2 + 4 * 1024 * 4 + 2 * 4 * 32 * 128 * 2
+        gb = b8 / (ms * 1e-3) / 1e9
+        res["cfg4_fp8_paged_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
+                                        "frac_hbm": round(gb / PEAK_HBM_GBS, 4),
+                                        "caches_flushed": "read of 512 MiB", "bytes": b8}
+        del kc8, vc8
         # Several query rows per sequence over the cfg4 cache (speculative /
         # chunked decode): 4 rows, bottom-right causal.
         q4 = torch.randn(4, 32, 4, 128, generator=_gen(2)).half().cuda()

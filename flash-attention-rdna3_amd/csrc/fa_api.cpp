@@ -179,8 +179,12 @@ int fa_decode_paged(const fa_paged_params* params, void* stream) {
   if (p.num_splits < 1 || p.num_splits > 64) return fail(FA_ERR_INVALID, "fa_decode_paged: num_splits");
   if (p.seqlen_q < 1) return fail(FA_ERR_INVALID, "fa_decode_paged: seqlen_q must be >= 1");
   if (p.causal != 0 && p.causal != 1) return fail(FA_ERR_INVALID, "fa_decode_paged: causal must be 0 or 1");
-  if (!rows_ok(p.q, p.q_stride, 4, 2) || !rows_ok(p.k_cache, p.k_stride, 4, 2) ||
-      !rows_ok(p.v_cache, p.v_stride, 4, 2) || !rows_ok(p.out, p.out_stride, 4, 2))
+  if (p.kv_fp8 != 0 && p.kv_fp8 != 1) return fail(FA_ERR_INVALID, "fa_decode_paged: kv_fp8 must be 0 or 1");
+  if (p.kv_fp8 && (p.head_dim > 128 || p.block_size < 16))
+    return fail(FA_ERR_UNSUPPORTED, "fa_decode_paged: fp8 caches need head_dim <= 128 and block_size >= 16");
+  const int kes = p.kv_fp8 ? 1 : 2;
+  if (!rows_ok(p.q, p.q_stride, 4, 2) || !rows_ok(p.k_cache, p.k_stride, 4, kes) ||
+      !rows_ok(p.v_cache, p.v_stride, 4, kes) || !rows_ok(p.out, p.out_stride, 4, 2))
     return fail(FA_ERR_INVALID, "fa_decode_paged: q/caches/out need a unit last stride and 16-byte aligned rows");
   if (!p.block_table || !p.context_lens) return fail(FA_ERR_INVALID, "fa_decode_paged: metadata is NULL");
   if (!p.workspace || !aligned16(p.workspace)) return fail(FA_ERR_INVALID, "fa_decode_paged: workspace");

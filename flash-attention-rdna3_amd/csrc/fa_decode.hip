@@ -324,10 +324,7 @@ static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
       const int group = a.heads_q / a.heads_kv;
       const int nrb = (group * a.seqlen_q + 15) / 16;
       dim3 grid(a.num_splits, a.batch * a.heads_kv * nrb);
-      auto kern = decode2_kernel<Tag, D, PAGED ? 1 : 0>;
-      if constexpr (!PAGED) {
-        if (a.kv8) kern = decode2_kernel<Tag, D, 0, true>;
-      }
+      auto kern = a.kv8 ? decode2_kernel<Tag, D, PAGED ? 1 : 0, true> : decode2_kernel<Tag, D, PAGED ? 1 : 0>;
       hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(kern, grid, dim3(C::NT), C::LDS_BYTES, stream, a);
@@ -338,7 +335,7 @@ static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
       return hipGetLastError();
     }
   }
-  if (a.kv8) return hipErrorInvalidValue;  // fp8 caches: contiguous, head_dim <= 128 only
+  if (a.kv8) return hipErrorInvalidValue;  // fp8 caches: head_dim <= 128 and pages of >= 16 keys
   using C = DecCfg<Tag, D>;
   auto kern = decode_kernel<Tag, D, PAGED>;
   hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
@@ -433,7 +430,9 @@ hipError_t launch_paged(const fa_paged_params& p, hipStream_t s) {
   a.scale_log2 = p.softmax_scale * kLog2e;
   a.num_splits = p.num_splits;
   a.causal = p.causal ? 1 : 0;
-  a.out_scale = 1.f;
+  a.kv8 = p.kv_fp8 ? 1 : 0;
+  a.scale_log2 = p.softmax_scale * (a.kv8 ? p.k_scale : 1.f) * kLog2e;
+  a.out_scale = a.kv8 ? p.v_scale : 1.f;
   split_workspace(a, p.workspace);
   return decode_dispatch<true>(p.dtype, a, s);
 }

@@ -55,8 +55,17 @@ struct Dec2Cfg {
 #ifndef FA_DEC_SLOT_VGPRS
 #define FA_DEC_SLOT_VGPRS 128
 #endif
-  // A load is 16 bytes (8 16-bit elements) or, for an fp8 cache, 8 bytes.
-  static constexpr int NBUF = FA_DEC_SLOT_VGPRS / ((KV8 ? 2 : 4) * PER);
+  // fp8 cache: 16-byte loads of 16 elements.  K steps go in pairs (KP) when
+  // NSTEP is even (else one 8-byte load per step); V rows in 16-element
+  // pieces (VN loads per chunk per lane).
+  static constexpr bool KP = KV8 && NSTEP % 2 == 0;
+  static constexpr int KN = KP ? NSTEP / 2 : NSTEP;   // K loads per key block
+  static constexpr int VN = KV8 ? CK * (D / 16) / 64 : VLOADS;
+  static constexpr int SLOT_REGS = KV8 ? 2 * KN * (KP ? 4 : 2) + 4 * VN : 4 * PER;
+#ifndef FA_DEC_SLOT_VGPRS8
+#define FA_DEC_SLOT_VGPRS8 128
+#endif
+  static constexpr int NBUF = (KV8 ? FA_DEC_SLOT_VGPRS8 : FA_DEC_SLOT_VGPRS) / SLOT_REGS;
   static constexpr int WAVE_ELEMS = TILE;            // one private V tile per wave
   static constexpr int LOOP_BYTES = NW * WAVE_ELEMS * 2;
   static constexpr int OLD = 17;                     // merge buffer row stride (floats)
@@ -65,6 +74,7 @@ struct Dec2Cfg {
 };
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Eight fp8 (OCP e4m3) cache elements -> an 8-element 16-bit operand of the
 // query's type.  The conversion is exact (e4m3 values are representable in
@@ -103,17 +113,18 @@ __device__ inline s16x8 fp8x8_to_op(u32x2 r) {
 // ordinary vector loads into registers: the compiler's per-register vmcnt
 // tracking then waits exactly for the slot being used.  (Asynchronous LDS DMA
 // in this loop makes it drain every load at the loop head instead.)
-// KV8: the contiguous cache holds fp8 (OCP e4m3) K and V.
+// KV8: the cache holds fp8 (OCP e4m3) K and V.
 template <typename Tag, int D, int PAGE, bool KV8 = false>
 __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
   static_assert(PAGE == 0 || PAGE == 1, "decode2 handles contiguous and >=16-key pages");
-  static_assert(!(KV8 && PAGE), "fp8 caches are contiguous");
   constexpr bool PAGED = PAGE != 0;
   using C = Dec2Cfg<D, KV8>;
   using EL = Elem<Tag>;
   using S = uint16_t;
-  using KE = typename std::conditional<KV8, uint8_t, S>::type;   // cache element
-  using KRaw = typename std::conditional<KV8, u32x2, s16x8>::type;  // one load: 8 elements
+  using KE = typename std::conditional<KV8, uint8_t, S>::type;  // cache element
+  // Registers of one K / V load (see Dec2Cfg: KP, KN, VN).
+  using KRaw = typename std::conditional<KV8, typename std::conditional<C::KP, u32x4, u32x2>::type, s16x8>::type;
+  using VRaw = typename std::conditional<KV8, u32x4, s16x8>::type;
   extern __shared__ __align__(16) unsigned char smem_raw[];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -146,7 +157,13 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
   {
     const S* qrow = reinterpret_cast<const S*>(a.q) + b * a.q_stride[0] + hq * a.q_stride[1] + mq * a.q_stride[2];
 #pragma unroll
-    for (int s = 0; s < C::NSTEP; ++s) qop[s] = load_op<Tag>(qrow + 8 * (4 * s + g4));
+    for (int s = 0; s < C::NSTEP; ++s) {
+      // With paired fp8 K loads, lane group g4 covers the 16 dims
+      // 64*(s/2) + 16*g4 of a step pair (a permutation of the contracted
+      // index, applied to Q and K alike).
+      const int d0 = C::KP ? 64 * (s / 2) + 16 * g4 + 8 * (s % 2) : 8 * (4 * s + g4);
+      qop[s] = load_op<Tag>(qrow + d0);
+    }
     wait_vm_all();
     if (!rvalid) {
 #pragma unroll
@@ -198,9 +215,9 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
 
   // Chunk slot j: K registers kr[j], V registers vr[j].  `live` false loads
   // the stand-in row 0 (nothing of it is used).
-  KRaw kr[C::NBUF][2][C::NSTEP];
-  KRaw vreg[C::NBUF][C::VLOADS];
-  auto issue_chunk = [&](int c, bool live, KRaw (&kd)[2][C::NSTEP], KRaw (&vd)[C::VLOADS]) {
+  KRaw kr[C::NBUF][2][C::KN];
+  VRaw vreg[C::NBUF][C::VN];
+  auto issue_chunk = [&](int c, bool live, KRaw (&kd)[2][C::KN], VRaw (&vd)[C::VN]) {
     const int n0 = c * C::CK;
     int pg0 = 0, pg1 = 0;
     if constexpr (PAGE == 1) chunk_pages(c, pg0, pg1);
@@ -209,18 +226,21 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
       int64_t ko = key_off(n0 + 16 * kb + l16, pg0, pg1, a.k_stride);
       ko = (ko < 0 || !live) ? 0 : ko;
 #pragma unroll
-      for (int s = 0; s < C::NSTEP; ++s) {
-        if constexpr (KV8) kd[kb][s] = *reinterpret_cast<const u32x2*>(kbase + ko + 8 * (4 * s + g4));
+      for (int s = 0; s < C::KN; ++s) {
+        if constexpr (C::KP) kd[kb][s] = *reinterpret_cast<const u32x4*>(kbase + ko + 64 * s + 16 * g4);
+        else if constexpr (KV8) kd[kb][s] = *reinterpret_cast<const u32x2*>(kbase + ko + 8 * (4 * s + g4));
         else kd[kb][s] = load_op<Tag>(kbase + ko + 8 * (4 * s + g4));
       }
     }
+    // V: 8-element (16-bit) or 16-element (fp8) pieces of the chunk's rows.
+    constexpr int PPR = KV8 ? D / 16 : C::CPR;  // pieces per row
 #pragma unroll
-    for (int i = 0; i < C::VLOADS; ++i) {
+    for (int i = 0; i < C::VN; ++i) {
       const int slot = 64 * i + lane;
-      const int row = slot / C::CPR;
+      const int row = slot / PPR;
       int64_t vo = key_off(n0 + row, pg0, pg1, a.v_stride);
       vo = (vo < 0 || !live) ? 0 : vo;
-      vd[i] = *reinterpret_cast<const KRaw*>(vbase + vo + (slot % C::CPR) * 8);
+      vd[i] = *reinterpret_cast<const VRaw*>(vbase + vo + (slot % PPR) * (KV8 ? 16 : 8));
     }
   };
   // Bit k of the result: key n0 + k of the chunk is visible.
@@ -238,25 +258,38 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
   for (int i = 0; i < C::NDB; ++i) acc[i] = f32x4v{0.f, 0.f, 0.f, 0.f};
 
   S* const Vs = wbase;
-  auto to_op = [&](const KRaw& r) -> s16x8 {
-    if constexpr (KV8) return fp8x8_to_op<Tag>(r);
-    else return r;
+  // K operand of step s of key block kb.
+  auto k_op = [&](const KRaw (&kd)[2][C::KN], int kb, int s) -> s16x8 {
+    if constexpr (C::KP) {
+      const u32x4 w = kd[kb][s / 2];
+      return fp8x8_to_op<Tag>(s % 2 ? u32x2{w[2], w[3]} : u32x2{w[0], w[1]});
+    } else if constexpr (KV8) {
+      return fp8x8_to_op<Tag>(kd[kb][s]);
+    } else {
+      return kd[kb][s];
+    }
   };
-  auto compute_chunk = [&](int c, const KRaw (&kd)[2][C::NSTEP], const KRaw (&vd)[C::VLOADS]) {
+  auto compute_chunk = [&](int c, const KRaw (&kd)[2][C::KN], const VRaw (&vd)[C::VN]) {
     const uint32_t vmask = chunk_mask(c);
     // V rows -> this wave's LDS tile (swizzled); the previous chunk's reads of
     // the tile precede these writes in the wave's LDS order.
 #pragma unroll
-    for (int i = 0; i < C::VLOADS; ++i) {
+    for (int i = 0; i < C::VN; ++i) {
       const int slot = 64 * i + lane;
-      *reinterpret_cast<s16x8*>(Vs + swz_off<D>(slot / C::CPR, (slot % C::CPR) * 8)) = to_op(vd[i]);
+      if constexpr (KV8) {
+        const int row = slot / (D / 16), col = (slot % (D / 16)) * 16;
+        *reinterpret_cast<s16x8*>(Vs + swz_off<D>(row, col)) = fp8x8_to_op<Tag>(u32x2{vd[i][0], vd[i][1]});
+        *reinterpret_cast<s16x8*>(Vs + swz_off<D>(row, col + 8)) = fp8x8_to_op<Tag>(u32x2{vd[i][2], vd[i][3]});
+      } else {
+        *reinterpret_cast<s16x8*>(Vs + swz_off<D>(slot / C::CPR, (slot % C::CPR) * 8)) = vd[i];
+      }
     }
     f32x4v sacc[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       sacc[kb] = f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < C::NSTEP; ++s) sacc[kb] = mma16<Tag>(to_op(kd[kb][s]), qop[s], sacc[kb]);
+      for (int s = 0; s < C::NSTEP; ++s) sacc[kb] = mma16<Tag>(k_op(kd, kb, s), qop[s], sacc[kb]);
     }
     float tmax = kNegInf;
 #pragma unroll

@@ -98,7 +98,8 @@ class PagedParams(ctypes.Structure):
         ("max_blocks", ctypes.c_int32), ("num_splits", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float), ("seqlen_q", ctypes.c_int32),
         ("workspace", ctypes.c_void_p),
-        ("causal", ctypes.c_int32), ("reserved0", ctypes.c_int32),
+        ("causal", ctypes.c_int32), ("kv_fp8", ctypes.c_int32),
+        ("k_scale", ctypes.c_float), ("v_scale", ctypes.c_float),
     ]
 
 

@@ -525,12 +525,7 @@ def flash_attention_decode(query, key, value, softmax_scale=None, *, cache_seqle
 def _validate_fp8_kv(query, key, value, k_scale, v_scale):
     """Contracts of an fp8 (e4m3) KV cache: the dense shape rules, checked on
     16-bit stand-ins of the same shapes, plus the fp8-specific ones."""
-    if not isinstance(value, torch.Tensor) or value.dtype != torch.float8_e4m3fn:
-        raise ValueError("key and value must both be float8_e4m3fn caches")
-    for name, sc in (("k_scale", k_scale), ("v_scale", v_scale)):
-        if sc is not None and (isinstance(sc, bool) or not isinstance(sc, (int, float))
-                               or not math.isfinite(float(sc)) or float(sc) <= 0.0):
-            raise ValueError(f"{name} must be a positive finite number or None")
+    _check_fp8_pair(value, k_scale, v_scale)
     if not isinstance(query, torch.Tensor) or query.dtype not in LOW_PRECISION_DTYPES:
         raise ValueError("query must be float16 or bfloat16 with an fp8 KV cache")
     stand_in = lambda t: torch.empty_strided(t.shape, [0] * t.dim(), dtype=query.dtype, device=t.device)
@@ -764,7 +759,8 @@ def flash_attention_varlen(query, key, value, cu_seqlens_q, cu_seqlens_k,
 # ---------------------------------------------------------------------------
 
 def flash_attention_decode_paged(query, k_cache, v_cache, block_table, context_lens,
-                                 softmax_scale=None, *, max_context_len=None, num_splits=None):
+                                 softmax_scale=None, *, max_context_len=None, num_splits=None, k_scale=None,
+                                 v_scale=None):
     """Decode attention over a paged (block-table) KV cache, vLLM style.
 
     Args:
@@ -778,14 +774,44 @@ def flash_attention_decode_paged(query, k_cache, v_cache, block_table, context_l
 
     Returns:
         ``(batch, q_heads, head_dim)``.  Non-causal, inference-only.
+
+    ``k_cache`` / ``v_cache`` may be ``torch.float8_e4m3fn`` caches holding
+    K / k_scale and V / v_scale (head_dim <= 128, block_size >= 16; an
+    MI355X-build extension, see :func:`flash_attention_decode`).
     """
-    validate_paged_inputs(query, k_cache, v_cache, block_table, context_lens)
+    fp8 = _validate_paged(query, k_cache, v_cache, block_table, context_lens, k_scale, v_scale)
     validate_inference_only(query, k_cache, v_cache)
     validate_softmax_scale(softmax_scale)
     _paged_options(max_context_len, num_splits)
     out = _paged_launch(query.unsqueeze(2), k_cache, v_cache, block_table, context_lens, softmax_scale,
-                        max_context_len, num_splits, causal=False)
+                        max_context_len, num_splits, causal=False, fp8_scales=fp8)
     return out.squeeze(2)
+
+
+def _validate_paged(query, k_cache, v_cache, block_table, context_lens, k_scale, v_scale):
+    """Paged contracts; returns (k_scale, v_scale) for fp8 caches, else None."""
+    if not (isinstance(k_cache, torch.Tensor) and k_cache.dtype == torch.float8_e4m3fn):
+        if k_scale is not None or v_scale is not None:
+            raise ValueError("k_scale and v_scale apply to float8_e4m3fn key / value caches only")
+        validate_paged_inputs(query, k_cache, v_cache, block_table, context_lens)
+        return None
+    _check_fp8_pair(v_cache, k_scale, v_scale)
+    if not isinstance(query, torch.Tensor) or query.dtype not in LOW_PRECISION_DTYPES:
+        raise ValueError("query must be float16 or bfloat16 with an fp8 KV cache")
+    stand_in = lambda t: torch.empty_strided(t.shape, [0] * t.dim(), dtype=query.dtype, device=t.device)
+    validate_paged_inputs(query, stand_in(k_cache), stand_in(v_cache), block_table, context_lens)
+    if query.shape[-1] not in (32, 64, 128) or k_cache.shape[1] < 16:
+        raise ValueError("fp8 paged caches need head_dim 32, 64 or 128 and block_size >= 16")
+    return (1.0 if k_scale is None else float(k_scale), 1.0 if v_scale is None else float(v_scale))
+
+
+def _check_fp8_pair(value, k_scale, v_scale):
+    if not isinstance(value, torch.Tensor) or value.dtype != torch.float8_e4m3fn:
+        raise ValueError("key and value must both be float8_e4m3fn caches")
+    for name, sc in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if sc is not None and (isinstance(sc, bool) or not isinstance(sc, (int, float))
+                               or not math.isfinite(float(sc)) or float(sc) <= 0.0):
+            raise ValueError(f"{name} must be a positive finite number or None")
 
 
 def _paged_options(max_context_len, num_splits):
@@ -800,7 +826,7 @@ def _paged_options(max_context_len, num_splits):
 
 
 def _paged_launch(query, k_cache, v_cache, block_table, context_lens, softmax_scale, max_context_len,
-                  num_splits, causal):
+                  num_splits, causal, fp8_scales=None):
     """Paged decode launch for a (batch, q_heads, Sq, head_dim) query (arguments
     already validated)."""
     max_context_len = None if max_context_len is None else int(max_context_len)
@@ -820,7 +846,11 @@ def _paged_launch(query, k_cache, v_cache, block_table, context_lens, softmax_sc
         splits = int(_paged_num_splits(batch, q_heads, block_size, block_table.shape[1],
                                        2 * _cu_count(query.device), max_context_len=max_context_len,
                                        requested_splits=num_splits))
-    q, kc, vc = _prep(_pad_head_dim(query, kdim), _pad_head_dim(k_cache, kdim), _pad_head_dim(v_cache, kdim))
+    if fp8_scales is not None:
+        q, kc, vc = _prep(query, k_cache, v_cache)  # head_dim is a kernel dim: no padding
+    else:
+        q, kc, vc = _prep(_pad_head_dim(query, kdim), _pad_head_dim(k_cache, kdim),
+                          _pad_head_dim(v_cache, kdim))
     out = torch.empty((batch, q_heads, seqlen_q, kdim), dtype=query.dtype, device=query.device)
     workspace = torch.empty(_native.decode_workspace_bytes(batch, q_heads, seqlen_q, kdim, splits),
                             dtype=torch.uint8, device=query.device)
@@ -841,13 +871,17 @@ def _paged_launch(query, k_cache, v_cache, block_table, context_lens, softmax_sc
     p.softmax_scale = softmax_scale
     p.seqlen_q = seqlen_q
     p.causal = 1 if causal else 0
+    if fp8_scales is not None:
+        p.kv_fp8 = 1
+        p.k_scale, p.v_scale = fp8_scales
     p.workspace = workspace.data_ptr()
     _native.call("fa_decode_paged", p, query)
     return out[..., :head_dim] if kdim != head_dim else out
 
 
 def flash_attention_decode_paged_multi(query, k_cache, v_cache, block_table, context_lens, softmax_scale=None,
-                                       *, causal=True, max_context_len=None, num_splits=None):
+                                       *, causal=True, max_context_len=None, num_splits=None, k_scale=None,
+                                       v_scale=None):
     """Paged decode of several query rows per sequence (speculative or chunked
     decode over a vLLM-style cache; no counterpart in the reference, whose
     paged decode takes one row, interface.py:643-728).
@@ -859,12 +893,12 @@ def flash_attention_decode_paged_multi(query, k_cache, v_cache, block_table, con
     Returns ``(batch, q_heads, Sq, head_dim)``.  Inference-only.
     """
     _require_4d_query(query)
-    validate_paged_inputs(query.select(2, 0), k_cache, v_cache, block_table, context_lens)
+    fp8 = _validate_paged(query.select(2, 0), k_cache, v_cache, block_table, context_lens, k_scale, v_scale)
     validate_inference_only(query, k_cache, v_cache)
     validate_softmax_scale(softmax_scale)
     _paged_options(max_context_len, num_splits)
     return _paged_launch(query, k_cache, v_cache, block_table, context_lens, softmax_scale, max_context_len,
-                         num_splits, causal=bool(causal))
+                         num_splits, causal=bool(causal), fp8_scales=fp8)
 
 
 def _require_4d_query(query):

@@ -243,7 +243,10 @@ typedef struct fa_paged_params {
   int32_t seqlen_q; /* query rows per sequence, >= 1 */
   void* workspace; /* fa_decode_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits) */
   int32_t causal;  /* 0 or 1 */
-  int32_t reserved0;
+  int32_t kv_fp8;  /* 1: caches are fp8 (OCP e4m3) holding K / k_scale and V / v_scale
+                      (head_dim <= 128, block_size >= 16); 0: they have `dtype` */
+  float k_scale;
+  float v_scale;
 } fa_paged_params;
 
 /*

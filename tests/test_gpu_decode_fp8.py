@@ -61,3 +61,25 @@ def test_fp8_strided_cache_is_copied_to_rows():
     out = flash_attention_decode(q.to(DEVICE), kt, v.to(DEVICE))
     ref = oracle.decode(q.float().numpy(), k.float().numpy(), v.float().numpy())
     np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=2e-3, rtol=0)
+
+
+@pytest.mark.parametrize("P", [16, 64])
+@pytest.mark.parametrize("Sq", [1, 4])
+def test_fp8_paged_decode_matches_oracle(P, Sq):
+    from fa_rdna3 import flash_attention_decode_paged, flash_attention_decode_paged_multi
+    g = torch.Generator().manual_seed(P + Sq)
+    B, Hq, Hkv, D, mb = 3, 32, 8, 128, 2048 // P
+    nb = B * mb + 5
+    q = torch.randn(B, Hq, Sq, D, generator=g).half()
+    kc = (torch.randn(nb, P, Hkv, D, generator=g) / 0.5).to(torch.float8_e4m3fn)
+    vc = (torch.randn(nb, P, Hkv, D, generator=g) / 2.0).to(torch.float8_e4m3fn)
+    bt = torch.randperm(nb, generator=g)[:B * mb].reshape(B, mb).to(torch.int32)
+    ctx = torch.tensor([9, 1500, 2048], dtype=torch.int32)
+    args = (kc.to(DEVICE), vc.to(DEVICE), bt.to(DEVICE), ctx.to(DEVICE))
+    if Sq == 1:
+        out = flash_attention_decode_paged(q[:, :, 0].to(DEVICE), *args, k_scale=0.5, v_scale=2.0)[:, :, None]
+    else:
+        out = flash_attention_decode_paged_multi(q.to(DEVICE), *args, causal=True, k_scale=0.5, v_scale=2.0)
+    ref = oracle.paged_attention(q.float().numpy(), kc.float().numpy() * 0.5, vc.float().numpy() * 2.0,
+                                 bt.numpy(), ctx.numpy(), causal=Sq > 1)
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=4e-3, rtol=0)
