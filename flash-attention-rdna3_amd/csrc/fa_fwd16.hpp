@@ -128,10 +128,13 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
   DmaSwzTile<C::BN, D, C::NTH> kt, vt;
   kt.init(ks, htid);
   vt.init(vs, htid);
-  // Key tiles [0, nh0) go to half 0, [nh0, ntiles) to half 1; both halves
-  // run nh0 steps so their barriers line up.
+  // Both halves run nh0 steps so their barriers line up.
   const int nh0 = (ntiles + 1) / 2;
-  const int my_first = khalf == 0 ? 0 : nh0;
+  // Half 0 takes the even key tiles, half 1 the odd ones: the two masked
+  // diagonal tiles of a causal block then fall into the same step instead of
+  // two steps in which half 0 waits for half 1.
+  const int my_first = khalf;
+  constexpr int TSTEP = 2;
   const int my_count = khalf == 0 ? nh0 : ntiles - nh0;
   const uint32_t lds0 = lds_addr(smem) + (uint32_t)(khalf * C::HALF) * 2u;
   // Tile sources advance by BN rows per load (scalar pointer arithmetic).
@@ -143,9 +146,9 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
     const uint32_t base = lds0 + (uint32_t)(stage * C::STAGE) * 2u;
     kt.load(rows_rsrc_words<D>(k_next, ks, rows), base, wave);
     vt.load(rows_rsrc_words<D>(v_next, vs, rows), base + C::KTILE * 2u, wave);
-    n_next += C::BN;
-    k_next += (int64_t)C::BN * ks;
-    v_next += (int64_t)C::BN * vs;
+    n_next += TSTEP * C::BN;
+    k_next += (int64_t)(TSTEP * C::BN) * ks;
+    v_next += (int64_t)(TSTEP * C::BN) * vs;
   };
   const VisBounds vbnd = row_block_bounds(md, m0w, mrows);
 
@@ -154,7 +157,7 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
   __syncthreads();
 
   for (int t = 0; t < nh0; ++t) {
-    const int n0 = lo + (my_first + t) * C::BN;
+    const int n0 = lo + (my_first + TSTEP * t) * C::BN;
     const int stage = t & 1;
     const int vis = t < my_count ? bounds_vis(vbnd, n0, n0 + C::BN - 1) : 0;
     if (!vis && t + 1 < my_count) load_tiles(stage ^ 1);
