@@ -245,16 +245,19 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
         if constexpr (MODE == 0) sched_read_ahead<2 * C::NSTEP, 4, 2, 8>();
         // The fully visible case (no modifiers) is its own straight-line
         // body: a per-element choice would become one branch per score.
-        auto scores = [&](auto plain_t, auto cap_t, auto bias_t, auto alibi_t) {
+        // MASK: the block is partly visible (vis == 1); fully visible blocks
+        // skip the per-score visibility test.
+        auto scores = [&](auto plain_t, auto cap_t, auto bias_t, auto alibi_t, auto mask_t) {
           constexpr bool plain = decltype(plain_t)::value;
           constexpr bool CAP = decltype(cap_t)::value;
+          constexpr bool MASK = decltype(mask_t)::value;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             float pv, tc = 0.f;
             if constexpr (MODE == 0) {
               // sacc = s - lse2/c, pacc = dP - delta (seeded accumulators).
               pv = __builtin_amdgcn_exp2f(sacc[i] * c);
-              if constexpr (!plain) pv = ((vis == 1) & !keep_pos(md, m0 + acc_row(i, h), n)) ? 0.f : pv;
+              if constexpr (MASK) pv = !keep_pos(md, m0 + acc_row(i, h), n) ? 0.f : pv;
             } else {
               const int m = m0 + acc_row(i, h);
               const float x = score_m<CAP, decltype(bias_t)::value, decltype(alibi_t)::value>(md, sacc[i], m, n, tc);
@@ -262,7 +265,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
               // the stage (register pressure of the modifier variants).
               const float l2i = L2[8 * (i / 4) + 4 * h + (i % 4)];
               pv = __builtin_amdgcn_exp2f(x - l2i);
-              pv = ((vis == 1) & !keep_pos(md, m, n)) ? 0.f : pv;
+              if constexpr (MASK) pv = !keep_pos(md, m, n) ? 0.f : pv;
             }
             float dp = pacc[i], pd = pv;
             if constexpr (MODE == 2) {
@@ -278,12 +281,14 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
             pacc[i] = ds;
           }
         };
+        using T_ = std::true_type;
         using F_ = std::false_type;
         if constexpr (MODE >= 1) {
-          dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_); });
+          if (vis == 1) dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_, T_{}); });
+          else dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_, F_{}); });
         } else {
-          if (vis == 2) scores(std::true_type{}, F_{}, std::integral_constant<int, 0>{}, F_{});
-          else scores(F_{}, F_{}, std::integral_constant<int, 0>{}, F_{});
+          if (vis == 2) scores(T_{}, F_{}, std::integral_constant<int, 0>{}, F_{}, F_{});
+          else scores(F_{}, F_{}, std::integral_constant<int, 0>{}, F_{}, T_{});
         }
         s16x8 pb[C::NPV], sb[C::NPV];
 #pragma unroll
@@ -539,9 +544,12 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
           pacc[kb2] = EL::mma(swz_op<D>(Vs, kb2 * 32 + l32, 2 * s + h), gop[s], pacc[kb2]);
         }
       if constexpr (MODE == 0) sched_read_ahead<2 * C::NSTEP * C::NKB, 4>();
-      auto scores = [&](auto plain_t, auto cap_t, auto bias_t, auto alibi_t) {
+      // MASK: the tile is partly visible (vis == 1); fully visible tiles
+      // skip the per-score visibility test.
+      auto scores = [&](auto plain_t, auto cap_t, auto bias_t, auto alibi_t, auto mask_t) {
         constexpr bool plain = decltype(plain_t)::value;
         constexpr bool CAP = decltype(cap_t)::value;
+        constexpr bool MASK = decltype(mask_t)::value;
 #pragma unroll
         for (int kb2 = 0; kb2 < C::NKB; ++kb2)
 #pragma unroll
@@ -553,7 +561,7 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
             } else {
               const float x = score_m<CAP, decltype(bias_t)::value, decltype(alibi_t)::value>(md, sacc[kb2][i], m, nn, tc);
               pv = __builtin_amdgcn_exp2f(x - lse2);
-              pv = ((vis == 1) & !keep_pos(md, m, nn)) ? 0.f : pv;
+              if constexpr (MASK) pv = !keep_pos(md, m, nn) ? 0.f : pv;
             }
             float dp = pacc[kb2][i];
             if constexpr (MODE == 2) {
@@ -564,12 +572,14 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
             sacc[kb2][i] = ds;
           }
       };
+      using T_ = std::true_type;
       using F_ = std::false_type;
       if constexpr (MODE >= 1) {
-        dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_); });
+        if (vis == 1) dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_, T_{}); });
+        else dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_, F_{}); });
       } else {
-        if (vis == 2) scores(std::true_type{}, F_{}, std::integral_constant<int, 0>{}, F_{});
-        else scores(F_{}, F_{}, std::integral_constant<int, 0>{}, F_{});
+        if (vis == 2) scores(T_{}, F_{}, std::integral_constant<int, 0>{}, F_{}, F_{});
+        else scores(F_{}, F_{}, std::integral_constant<int, 0>{}, F_{}, T_{});
       }
       s16x8 sb[C::NPV];
 #pragma unroll

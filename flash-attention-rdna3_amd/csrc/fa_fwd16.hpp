@@ -190,7 +190,9 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
         // This lane's visible keys (its row is fixed): one interval per tile.
         int klo = INT_MIN, khi = INT_MAX;
         if (vis == 1) key_bounds(md, m, klo, khi);
-        auto masked_scores = [&](auto cap_t, auto bias_t, auto alibi_t) {
+        // MASK: the tile is partly visible (vis == 1); a fully visible tile
+        // with modifiers skips the per-score interval test.
+        auto masked_scores = [&](auto cap_t, auto bias_t, auto alibi_t, auto mask_t) {
 #pragma unroll
           for (int kb2 = 0; kb2 < C::NKB; ++kb2)
 #pragma unroll
@@ -199,13 +201,22 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
               float tc;
               float x = score_m<decltype(cap_t)::value, decltype(bias_t)::value, decltype(alibi_t)::value>(
                   md, sacc[kb2][i], m, n, tc);
-              x = ((n >= klo) & (n <= khi)) ? x : kNegInf;
+              if constexpr (decltype(mask_t)::value) x = ((n >= klo) & (n <= khi)) ? x : kNegInf;
               sacc[kb2][i] = x;
               tmax = fmaxf(tmax, x);
             }
         };
-        if constexpr (MODE >= 1) dispatch_mods(md, masked_scores);
-        else masked_scores(std::false_type{}, std::integral_constant<int, 0>{}, std::false_type{});
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        if constexpr (MODE == 1) {
+          if (vis == 1) dispatch_mods(md, [&](auto a, auto b_, auto c_) { masked_scores(a, b_, c_, T_{}); });
+          else dispatch_mods(md, [&](auto a, auto b_, auto c_) { masked_scores(a, b_, c_, F_{}); });
+        } else if constexpr (MODE == 2) {
+          // (one variant: the dropout kernel has no registers to spare)
+          dispatch_mods(md, [&](auto a, auto b_, auto c_) { masked_scores(a, b_, c_, T_{}); });
+        } else {
+          masked_scores(F_{}, std::integral_constant<int, 0>{}, F_{}, T_{});
+        }
       }
       tmax = half_max(tmax);
       // Lazy rescale, decided for the whole wave.
