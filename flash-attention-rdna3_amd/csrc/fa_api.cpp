@@ -155,8 +155,6 @@ int fa_decode_splitk(const fa_decode_params* params, void* stream) {
     return fail(FA_ERR_INVALID, "fa_decode_splitk: bad shape");
   if (p.num_splits < 1 || p.num_splits > 64) return fail(FA_ERR_INVALID, "fa_decode_splitk: num_splits");
   if (p.kv_fp8 != 0 && p.kv_fp8 != 1) return fail(FA_ERR_INVALID, "fa_decode_splitk: kv_fp8 must be 0 or 1");
-  if (p.kv_fp8 && p.head_dim > 128)
-    return fail(FA_ERR_UNSUPPORTED, "fa_decode_splitk: fp8 caches need head_dim <= 128, got %d", p.head_dim);
   const int kes = p.kv_fp8 ? 1 : 2;
   if (!rows_ok(p.q, p.q_stride, 4, 2) || !rows_ok(p.k, p.k_stride, 4, kes) || !rows_ok(p.v, p.v_stride, 4, kes) ||
       !rows_ok(p.out, p.out_stride, 4, 2))
@@ -180,8 +178,6 @@ int fa_decode_paged(const fa_paged_params* params, void* stream) {
   if (p.seqlen_q < 1) return fail(FA_ERR_INVALID, "fa_decode_paged: seqlen_q must be >= 1");
   if (p.causal != 0 && p.causal != 1) return fail(FA_ERR_INVALID, "fa_decode_paged: causal must be 0 or 1");
   if (p.kv_fp8 != 0 && p.kv_fp8 != 1) return fail(FA_ERR_INVALID, "fa_decode_paged: kv_fp8 must be 0 or 1");
-  if (p.kv_fp8 && (p.head_dim > 128 || p.block_size < 16))
-    return fail(FA_ERR_UNSUPPORTED, "fa_decode_paged: fp8 caches need head_dim <= 128 and block_size >= 16");
   const int kes = p.kv_fp8 ? 1 : 2;
   if (!rows_ok(p.q, p.q_stride, 4, 2) || !rows_ok(p.k_cache, p.k_stride, 4, kes) ||
       !rows_ok(p.v_cache, p.v_stride, 4, kes) || !rows_ok(p.out, p.out_stride, 4, 2))

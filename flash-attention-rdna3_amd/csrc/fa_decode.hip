@@ -51,7 +51,7 @@ struct DecodeArgs {
   float scale_log2;
   int32_t num_splits;
   int32_t causal;       // bottom-right per sequence: row i sees keys <= len - Sq + i
-  int32_t kv8;          // contiguous fp8 (OCP e4m3) K/V, decode2 path only
+  int32_t kv8;          // fp8 (OCP e4m3) K/V cache
   float out_scale;      // multiplies the output (v_scale of an fp8 cache); 1 otherwise
   float* ws_o;          // [splits][B][Hq][Sq][D] fp32
   float* ws_lse;        // [splits][B][Hq][Sq] fp32
@@ -92,11 +92,13 @@ size_t decode_workspace_bytes(int batch, int heads_q, int seqlen_q, int head_dim
   return (bytes + 255) / 256 * 256;
 }
 
-template <typename Tag, int D, bool PAGED>
+// KV8: the cache holds fp8 (OCP e4m3) K and V, converted as the tiles load.
+template <typename Tag, int D, bool PAGED, bool KV8 = false>
 __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   using C = DecCfg<Tag, D>;
   using EL = Elem<Tag>;
   using S = typename EL::S;
+  using KE = typename std::conditional<KV8, uint8_t, S>::type;  // cache element
   using Op = typename EL::Op;
   extern __shared__ __align__(16) unsigned char smem_raw[];
 
@@ -137,8 +139,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     wait_vm_all();
   }
 
-  const S* kbase = reinterpret_cast<const S*>(a.k);
-  const S* vbase = reinterpret_cast<const S*>(a.v);
+  const KE* kbase = reinterpret_cast<const KE*>(a.k);
+  const KE* vbase = reinterpret_cast<const KE*>(a.v);
   if constexpr (!PAGED) {
     kbase += b * a.k_stride[0] + hk * a.k_stride[1];
     vbase += b * a.v_stride[0] + hk * a.v_stride[1];
@@ -161,14 +163,14 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
 
   S* ks = reinterpret_cast<S*>(smem_raw) + wave * C::WAVE_ELEMS;
   S* vs = ks + C::KT;
-  RowTile<Tag, C::CH, D, 64> kt;
-  TransTile<Tag, C::CH, C::DO, 64> vt;
+  RowTile<Tag, C::CH, D, 64, KV8> kt;
+  TransTile<Tag, C::CH, C::DO, 64, KV8> vt;
   uint32_t valid_next = 0, valid_cur = 0;
   auto load_chunk = [&](int c) {
     const int n0 = c * C::CH;
-    kt.load([&](int rr) -> const S* {
+    kt.load([&](int rr) -> const KE* {
       const int64_t o = key_off(n0 + rr, a.k_stride); return o < 0 ? nullptr : kbase + o; }, kbase, lane);
-    vt.load([&](int rr) -> const S* {
+    vt.load([&](int rr) -> const KE* {
       const int64_t o = key_off(n0 + rr, a.v_stride); return o < 0 ? nullptr : vbase + o + dc * C::DO; }, vbase + dc * C::DO, lane);
     valid_next = (uint32_t)__ballot(l32 == lane && key_off(n0 + l32, a.k_stride) >= 0);
   };
@@ -270,7 +272,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
       o += ow[(w * C::DO + d) * C::OLD + rr] * sc;
     }
     const float Ls = (L == 0.f) ? 1.f : L;
-    o /= Ls;
+    o = o / Ls * a.out_scale;  // out_scale: v_scale of an fp8 cache, else 1
     const int gg = row / a.seqlen_q, mm = row - gg * a.seqlen_q;
     const int hh = hk * group + gg;
     const int dd = dc * C::DO + d;
@@ -335,9 +337,8 @@ static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
       return hipGetLastError();
     }
   }
-  if (a.kv8) return hipErrorInvalidValue;  // fp8 caches: head_dim <= 128 and pages of >= 16 keys
   using C = DecCfg<Tag, D>;
-  auto kern = decode_kernel<Tag, D, PAGED>;
+  auto kern = a.kv8 ? decode_kernel<Tag, D, PAGED, true> : decode_kernel<Tag, D, PAGED>;
   hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
   if (e != hipSuccess) return e;
   const int group = a.heads_q / a.heads_kv;

@@ -73,33 +73,6 @@ struct Dec2Cfg {
   static constexpr int LDS_BYTES = LOOP_BYTES > MERGE_BYTES ? LOOP_BYTES : MERGE_BYTES;
 };
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Eight fp8 (OCP e4m3) cache elements -> an 8-element 16-bit operand of the
-// query's type.  The conversion is exact (e4m3 values are representable in
-// fp16 and bf16); the per-tensor scales are applied outside (k_scale in the
-// logit scale, v_scale on the output).
-template <typename Tag, bool HI>
-__device__ inline uint32_t fp8x2_to_16(uint32_t w) {
-  if constexpr (std::is_same<Tag, bf16_t>::value)
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, HI));
-  else
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, HI));
-}
-template <typename Tag>
-__device__ inline s16x8 fp8x8_to_op(u32x2 r) {
-  const uint32_t p[4] = {fp8x2_to_16<Tag, false>(r[0]), fp8x2_to_16<Tag, true>(r[0]),
-                         fp8x2_to_16<Tag, false>(r[1]), fp8x2_to_16<Tag, true>(r[1])};
-  s16x8 o;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    o[2 * i] = (short)(p[i] & 0xFFFFu);
-    o[2 * i + 1] = (short)(p[i] >> 16);
-  }
-  return o;
-}
-
 // PAGE: 0 contiguous cache; 1 paged with block_size >= 16 (a 32-key chunk
 // spans at most two pages, whose ids are wave-uniform scalar loads).
 //

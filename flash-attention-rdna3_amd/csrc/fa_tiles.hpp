@@ -28,7 +28,43 @@ __device__ inline uint4 masked(const uint4& x, uint32_t keep) {
   return make_uint4(x.x & m, x.y & m, x.z & m, x.w & m);
 }
 
-template <typename Tag, int R, int COLS, int NT>
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Eight fp8 (OCP e4m3) cache elements -> an 8-element 16-bit operand of the
+// query's type.  The conversion is exact (e4m3 values are representable in
+// fp16 and bf16); the per-tensor scales are applied outside (k_scale in the
+// logit scale, v_scale on the output).
+template <typename Tag, bool HI>
+__device__ inline uint32_t fp8x2_to_16(uint32_t w) {
+  if constexpr (std::is_same<Tag, bf16_t>::value)
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, HI));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w, 1.0f, HI));
+}
+template <typename Tag>
+__device__ inline s16x8 fp8x8_to_op(u32x2 r) {
+  const uint32_t p[4] = {fp8x2_to_16<Tag, false>(r[0]), fp8x2_to_16<Tag, true>(r[0]),
+                         fp8x2_to_16<Tag, false>(r[1]), fp8x2_to_16<Tag, true>(r[1])};
+  s16x8 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = (short)(p[i] & 0xFFFFu);
+    o[2 * i + 1] = (short)(p[i] >> 16);
+  }
+  return o;
+}
+
+// Eight fp8 cache elements at p (8-byte aligned) as one 16-byte chunk of
+// 16-bit elements of the query's type.
+template <typename Tag>
+__device__ inline uint4 fp8_chunk(const uint8_t* p) {
+  return __builtin_bit_cast(uint4, fp8x8_to_op<Tag>(*reinterpret_cast<const u32x2*>(p)));
+}
+
+
+// KV8: the rows hold fp8 (e4m3) elements, converted to Tag as they load.
+template <typename Tag, int R, int COLS, int NT, bool KV8 = false>
 struct RowTile {
   using EL = Elem<Tag>;
   using S = typename EL::S;
@@ -41,16 +77,17 @@ struct RowTile {
 
   // rowptr(row) returns the address of element 0 of that tile row, or nullptr
   // for a zero row; `fallback` is any readable row of the same tensor.
-  template <typename RowPtr>
-  __device__ inline void load(RowPtr rowptr, const S* fallback, int tid) {
+  template <typename RowPtr, typename P>
+  __device__ inline void load(RowPtr rowptr, const P* fallback, int tid) {
     ok = 0;
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
       const int c = tid + NT * j;
-      const S* p = (CH % NT == 0 || c < CH) ? rowptr(c / CPR) : nullptr;
+      const P* p = (CH % NT == 0 || c < CH) ? rowptr(c / CPR) : nullptr;
       ok |= (p != nullptr ? 1u : 0u) << j;
       p = p ? p : fallback;
-      r[j] = *reinterpret_cast<const uint4*>(p + (c % CPR) * CE);
+      if constexpr (KV8) r[j] = fp8_chunk<Tag>(p + (c % CPR) * CE);
+      else r[j] = *reinterpret_cast<const uint4*>(p + (c % CPR) * CE);
     }
   }
   __device__ inline void store(S* lds, int LD, int tid) const {
@@ -63,7 +100,7 @@ struct RowTile {
   }
 };
 
-template <typename Tag, int R, int COLS, int NT>
+template <typename Tag, int R, int COLS, int NT, bool KV8 = false>
 struct TransTile {
   using EL = Elem<Tag>;
   using S = typename EL::S;
@@ -74,8 +111,8 @@ struct TransTile {
   uint4 r[PT * 4];  // flat: (item j, row q) at 4*j + q
   uint32_t ok;
 
-  template <typename RowPtr>
-  __device__ inline void load(RowPtr rowptr, const S* fallback, int tid) {
+  template <typename RowPtr, typename P>
+  __device__ inline void load(RowPtr rowptr, const P* fallback, int tid) {
     ok = 0;
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
@@ -84,10 +121,11 @@ struct TransTile {
       const int rq = it / CPR, cc = it % CPR;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const S* p = in ? rowptr(4 * rq + q) : nullptr;
+        const P* p = in ? rowptr(4 * rq + q) : nullptr;
         ok |= (p != nullptr ? 1u : 0u) << (4 * j + q);
         p = p ? p : fallback;
-        r[4 * j + q] = *reinterpret_cast<const uint4*>(p + cc * CE);
+        if constexpr (KV8) r[4 * j + q] = fp8_chunk<Tag>(p + cc * CE);
+        else r[4 * j + q] = *reinterpret_cast<const uint4*>(p + cc * CE);
       }
     }
   }

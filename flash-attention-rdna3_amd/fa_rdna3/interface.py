@@ -493,8 +493,8 @@ def flash_attention_decode(query, key, value, softmax_scale=None, *, cache_seqle
     extension; absent, every key is visible as in the reference).
 
     ``key`` / ``value`` may also be ``torch.float8_e4m3fn`` caches holding
-    K / k_scale and V / v_scale (per-tensor scales, default 1; head_dim <= 128;
-    another MI355X-build extension): they are read as fp8, half the bytes of
+    K / k_scale and V / v_scale (per-tensor scales, default 1; head_dim 32, 64,
+    128, 256 or 512; another MI355X-build extension): they are read as fp8, half the bytes of
     a 16-bit cache, and converted exactly to the query's type in registers.
     """
     kv_fp8 = isinstance(key, torch.Tensor) and key.dtype == torch.float8_e4m3fn
@@ -522,6 +522,10 @@ def flash_attention_decode(query, key, value, softmax_scale=None, *, cache_seqle
     return _decode_launch(query, key, value, softmax_scale, cache_seqlens, causal=False)
 
 
+# fp8 caches are read at the kernel's own head dims (no padding of fp8 rows).
+_FP8_HEAD_DIMS = (32, 64, 128, 256, 512)
+
+
 def _validate_fp8_kv(query, key, value, k_scale, v_scale):
     """Contracts of an fp8 (e4m3) KV cache: the dense shape rules, checked on
     16-bit stand-ins of the same shapes, plus the fp8-specific ones."""
@@ -530,8 +534,8 @@ def _validate_fp8_kv(query, key, value, k_scale, v_scale):
         raise ValueError("query must be float16 or bfloat16 with an fp8 KV cache")
     stand_in = lambda t: torch.empty_strided(t.shape, [0] * t.dim(), dtype=query.dtype, device=t.device)
     validate_dense_inputs(query, stand_in(key), stand_in(value), dtypes=LOW_PRECISION_DTYPES)
-    if query.shape[3] not in (32, 64, 128):
-        raise ValueError(f"fp8 KV caches need head_dim 32, 64 or 128, got {query.shape[3]}")
+    if query.shape[3] not in _FP8_HEAD_DIMS:
+        raise ValueError(f"fp8 KV caches need head_dim 32, 64, 128, 256 or 512, got {query.shape[3]}")
 
 
 def _decode_launch(query, key, value, softmax_scale, lens, causal, lens_add=0, fp8_scales=None):
@@ -776,7 +780,7 @@ def flash_attention_decode_paged(query, k_cache, v_cache, block_table, context_l
         ``(batch, q_heads, head_dim)``.  Non-causal, inference-only.
 
     ``k_cache`` / ``v_cache`` may be ``torch.float8_e4m3fn`` caches holding
-    K / k_scale and V / v_scale (head_dim <= 128, block_size >= 16; an
+    K / k_scale and V / v_scale (head_dim 32, 64, 128, 256 or 512; an
     MI355X-build extension, see :func:`flash_attention_decode`).
     """
     fp8 = _validate_paged(query, k_cache, v_cache, block_table, context_lens, k_scale, v_scale)
@@ -800,8 +804,8 @@ def _validate_paged(query, k_cache, v_cache, block_table, context_lens, k_scale,
         raise ValueError("query must be float16 or bfloat16 with an fp8 KV cache")
     stand_in = lambda t: torch.empty_strided(t.shape, [0] * t.dim(), dtype=query.dtype, device=t.device)
     validate_paged_inputs(query, stand_in(k_cache), stand_in(v_cache), block_table, context_lens)
-    if query.shape[-1] not in (32, 64, 128) or k_cache.shape[1] < 16:
-        raise ValueError("fp8 paged caches need head_dim 32, 64 or 128 and block_size >= 16")
+    if query.shape[-1] not in _FP8_HEAD_DIMS:
+        raise ValueError("fp8 paged caches need head_dim 32, 64, 128, 256 or 512")
     return (1.0 if k_scale is None else float(k_scale), 1.0 if v_scale is None else float(v_scale))
 
 

@@ -163,8 +163,8 @@ typedef struct fa_decode_params {
   int32_t causal; /* 0 or 1, see above */
   int32_t cache_seqlens_add; /* added to every cache_seqlens[b] before clamping
                                 (rows just appended by fa_kvcache_append); 0 otherwise */
-  int32_t kv_fp8;  /* 1: k and v are fp8 (OCP e4m3) holding K / k_scale and V / v_scale
-                      (head_dim <= 128); 0: they have `dtype` and the scales are ignored */
+  int32_t kv_fp8;  /* 1: k and v are fp8 (OCP e4m3) holding K / k_scale and V / v_scale;
+                      0: they have `dtype` and the scales are ignored */
   float k_scale;
   float v_scale;
   int32_t reserved0;
@@ -243,8 +243,8 @@ typedef struct fa_paged_params {
   int32_t seqlen_q; /* query rows per sequence, >= 1 */
   void* workspace; /* fa_decode_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits) */
   int32_t causal;  /* 0 or 1 */
-  int32_t kv_fp8;  /* 1: caches are fp8 (OCP e4m3) holding K / k_scale and V / v_scale
-                      (head_dim <= 128, block_size >= 16); 0: they have `dtype` */
+  int32_t kv_fp8;  /* 1: caches are fp8 (OCP e4m3) holding K / k_scale and V / v_scale;
+                      0: they have `dtype` */
   float k_scale;
   float v_scale;
 } fa_paged_params;

@@ -175,9 +175,9 @@ def test_fp8_decode_contracts(monkeypatch):
     with pytest.raises(ValueError, match="k_scale"):
         flash_attention_decode(q, k8, k8.clone(), k_scale=0.0)
     with pytest.raises(ValueError, match="fp8 KV caches need head_dim"):
-        flash_attention_decode(torch.randn(2, 4, 1, 256, dtype=torch.float16),
-                               torch.randn(2, 2, 32, 256).to(torch.float8_e4m3fn),
-                               torch.randn(2, 2, 32, 256).to(torch.float8_e4m3fn))
+        flash_attention_decode(torch.randn(2, 4, 1, 80, dtype=torch.float16),
+                               torch.randn(2, 2, 32, 80).to(torch.float8_e4m3fn),
+                               torch.randn(2, 2, 32, 80).to(torch.float8_e4m3fn))
     with pytest.raises(ValueError, match="float8_e4m3fn key / value caches only"):
         flash_attention_decode(q, torch.randn(2, 2, 32, 64, dtype=torch.float16),
                                torch.randn(2, 2, 32, 64, dtype=torch.float16), v_scale=2.0)

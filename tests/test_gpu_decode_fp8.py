@@ -37,6 +37,19 @@ def test_fp8_decode_matches_oracle(qdtype, D, scales):
     np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=TOL[qdtype] * max(1.0, vs), rtol=0)
 
 
+@pytest.mark.parametrize("qdtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [256, 512])
+def test_fp8_decode_wide_heads_match_oracle(qdtype, D):
+    # head_dim > 128 runs the tiled split kernel with fp8 tiles.
+    q, k, v = _fp8_case(D + 3, 2, 8, 2, 3, 1100, D, 0.5, 2.0, qdtype)
+    lens = torch.tensor([1100, 37], dtype=torch.int32)
+    out = flash_attention_decode(q.to(DEVICE), k.to(DEVICE), v.to(DEVICE), cache_seqlens=lens.to(DEVICE),
+                                 k_scale=0.5, v_scale=2.0)
+    ref = oracle.decode(q.float().numpy(), k.float().numpy() * 0.5, v.float().numpy() * 2.0,
+                        cache_seqlens=lens.numpy())
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=2 * TOL[qdtype], rtol=0)
+
+
 def test_fp8_decode_query_rows_and_head_dim_32():
     q, k, v = _fp8_case(7, 2, 8, 2, 5, 777, 32, 1.0, 1.0, torch.float16)
     out = flash_attention_decode(q.to(DEVICE), k.to(DEVICE), v.to(DEVICE))
@@ -63,12 +76,14 @@ def test_fp8_strided_cache_is_copied_to_rows():
     np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=2e-3, rtol=0)
 
 
-@pytest.mark.parametrize("P", [16, 64])
+@pytest.mark.parametrize("P,D", [(16, 128), (64, 128), (8, 128), (4, 64), (16, 256)])
 @pytest.mark.parametrize("Sq", [1, 4])
-def test_fp8_paged_decode_matches_oracle(P, Sq):
+def test_fp8_paged_decode_matches_oracle(P, D, Sq):
+    # Pages of >= 16 keys with head_dim <= 128 take the streaming kernel;
+    # smaller pages and wider heads the tiled one.
     from fa_rdna3 import flash_attention_decode_paged, flash_attention_decode_paged_multi
-    g = torch.Generator().manual_seed(P + Sq)
-    B, Hq, Hkv, D, mb = 3, 32, 8, 128, 2048 // P
+    g = torch.Generator().manual_seed(P + Sq + D)
+    B, Hq, Hkv, mb = 3, 32, 8, 2048 // P
     nb = B * mb + 5
     q = torch.randn(B, Hq, Sq, D, generator=g).half()
     kc = (torch.randn(nb, P, Hkv, D, generator=g) / 0.5).to(torch.float8_e4m3fn)
