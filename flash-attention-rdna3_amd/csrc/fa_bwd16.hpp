@@ -248,7 +248,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
         // MASK: the block is partly visible (vis == 1); fully visible blocks
         // skip the per-score visibility test.
         auto scores = [&](auto plain_t, auto cap_t, auto bias_t, auto alibi_t, auto mask_t) {
-          constexpr bool plain = decltype(plain_t)::value;
+          (void)plain_t;  // the dK/dV body has no separate plain path
           constexpr bool CAP = decltype(cap_t)::value;
           constexpr bool MASK = decltype(mask_t)::value;
 #pragma unroll
