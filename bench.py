@@ -178,6 +178,18 @@ def run_cfg2(steps, warmup):
     return dt, (q, k, v, do, scale)
 
 
+def gemm_ceiling(n=8192, iters=10):
+    """The MFMA rate a library GEMM reaches on this GPU: torch.matmul
+    (hipBLASLt) on n x n x n fp16, HIP events, after warm-up.  Context for the
+    attention kernels' fraction of the 2.5 PF/s datasheet peak."""
+    a = torch.randn(n, n, device="cuda", dtype=torch.float16)
+    b = torch.randn(n, n, device="cuda", dtype=torch.float16)
+    for _ in range(3):
+        torch.matmul(a, b)
+    ms = _event_time(lambda: torch.matmul(a, b), iters, torch.cuda.current_stream())
+    return 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+
+
 def dkdv_roofline(tensors, iters=50):
     """Time the dK/dV kernel alone (fa_bwd phase 1) with HIP events."""
     from fa_rdna3 import interface as I
@@ -406,6 +418,10 @@ def main():
     }
     line["roofline"] = dkdv_roofline(tensors)
     if not args.no_extras:
+        ceil = gemm_ceiling()
+        line["mfma_gemm_ceiling"] = {
+            "value": round(ceil, 1), "unit": "TFLOP/s", "how": "torch.matmul fp16 8192^3 (hipBLASLt)",
+            "step_frac": round(value / ceil, 4), "dkdv_frac": round(line["roofline"]["achieved"] / ceil, 4)}
         line["decode"] = run_decode_configs()
         line["cfg5_varlen"] = run_cfg5()
     if not args.no_cpu_baseline:
