@@ -325,7 +325,7 @@ static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
       using C = Dec2Cfg<D>;
       const int group = a.heads_q / a.heads_kv;
       const int nrb = (group * a.seqlen_q + 15) / 16;
-      dim3 grid(a.heads_kv * nrb, a.num_splits * a.batch);
+      dim3 grid(a.heads_kv * nrb * a.num_splits, a.batch);
       auto kern = a.kv8 ? decode2_kernel<Tag, D, PAGED ? 1 : 0, true> : decode2_kernel<Tag, D, PAGED ? 1 : 0>;
       hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
       if (e != hipSuccess) return e;
