@@ -98,22 +98,15 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
   // operand) in LDS; the first barrier of the query loop publishes them.
   S* const klds = reinterpret_cast<S*>(smem_raw + 2 * C::HALF_BYTES) + wave * 32 * D;
   S* const vlds = klds + C::BN * D;
+  // The parked tiles are this wave's 32 key rows, row-major and swizzled:
+  // they go HBM -> LDS by DMA (rows past the sequence end read as zeros) in
+  // the same round trip as the first Q / dO stage.
   if (qhalf == 0) {
-    const S* kr = kbase + (int64_t)(nvalid ? n : 0) * f.k_stride[2] + 8 * h;
-    const S* vr = vbase + (int64_t)(nvalid ? n : 0) * f.v_stride[2] + 8 * h;
-    s16x8 kop[C::NSTEP], vop[C::NSTEP];
-#pragma unroll
-    for (int s = 0; s < C::NSTEP; ++s) {
-      kop[s] = load_op<Tag>(kr + 16 * s);
-      vop[s] = load_op<Tag>(vr + 16 * s);
-    }
-    wait_vm_all();
-#pragma unroll
-    for (int s = 0; s < C::NSTEP; ++s) {
-      const int off = swz_off<D>(l32, 8 * (2 * s + h));
-      *reinterpret_cast<s16x8*>(klds + off) = nvalid ? kop[s] : zero_op<Tag>();
-      *reinterpret_cast<s16x8*>(vlds + off) = nvalid ? vop[s] : zero_op<Tag>();
-    }
+    DmaSwzTile<32, D, 64> pk, pv;
+    pk.init(f.k_stride[2], lane);
+    pv.init(f.v_stride[2], lane);
+    pk.load(rows_rsrc_words<D>(kbase + (int64_t)n0w * f.k_stride[2], f.k_stride[2], ncols), lds_addr(klds), 0);
+    pv.load(rows_rsrc_words<D>(vbase + (int64_t)n0w * f.v_stride[2], f.v_stride[2], ncols), lds_addr(vlds), 0);
   }
 
   f32x16 dk[C::NDB], dv[C::NDB];
@@ -433,6 +426,52 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
   const bool mvalid = m < sq;
   s16x8 qop[C::NSTEP], gop[C::NSTEP];
   float lse2 = __builtin_inff(), dlt = 0.f;
+
+  f32x16 dq[C::NDB];
+#pragma unroll
+  for (int i = 0; i < C::NDB; ++i) dq[i] = zero16();
+
+  constexpr bool DMA = (C::BN * D / 8) % C::NTH == 0;
+  BufSwzTile<C::BN, D, C::NTH> kt, vt;
+  DmaSwzTile<C::BN, (DMA ? D : 64), C::NTH> kd, vd;
+  if constexpr (DMA) {
+    kd.init(ks, htid);
+    vd.init(vs, htid);
+  } else {
+    kt.init(ks, htid);
+    vt.init(vs, htid);
+  }
+  const int nh0 = (ntiles + 1) / 2;
+  const int my_first = khalf == 0 ? 0 : nh0;
+  const int my_count = khalf == 0 ? nh0 : ntiles - nh0;
+  S* const hsmem = smem + khalf * C::HALF;
+  const uint32_t lds0 = lds_addr(hsmem);
+  auto load_stage = [&](int n0, int st) {
+    const int rows = min(C::BN, sk - n0);
+    if constexpr (DMA) {
+      const uint32_t base = lds0 + (uint32_t)(st * C::STAGE) * 2u;
+      kd.load(rows_rsrc_words<D>(kbase + (int64_t)n0 * ks, ks, rows), base, wave);
+      vd.load(rows_rsrc_words<D>(vbase + (int64_t)n0 * vs, vs, rows), base + C::KT * 2u, wave);
+    } else {
+      kt.load(rows_rsrc<D>(kbase + (int64_t)n0 * ks, ks, rows));
+      vt.load(rows_rsrc<D>(vbase + (int64_t)n0 * vs, vs, rows));
+    }
+  };
+  auto store_stage = [&](int st) {
+    if constexpr (!DMA) {
+      S* base = hsmem + st * C::STAGE;
+      kt.store(base, htid);
+      vt.store(base + C::KT, htid);
+    }
+  };
+
+  const VisBounds qvb = row_block_bounds(md, m0w, mrows);
+  if (my_count > 0) {
+    load_stage(lo + my_first * C::BN, 0);
+    store_stage(0);
+  }
+  // The row operands load after the first K / V stage is issued: one round
+  // trip to memory for both.
   {
     const int mm = mvalid ? m : 0;
     const S* qr = reinterpret_cast<const S*>(f.q) + b * f.q_stride[0] + hq * f.q_stride[1] +
@@ -480,49 +519,6 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
     }
   }
 
-  f32x16 dq[C::NDB];
-#pragma unroll
-  for (int i = 0; i < C::NDB; ++i) dq[i] = zero16();
-
-  constexpr bool DMA = (C::BN * D / 8) % C::NTH == 0;
-  BufSwzTile<C::BN, D, C::NTH> kt, vt;
-  DmaSwzTile<C::BN, (DMA ? D : 64), C::NTH> kd, vd;
-  if constexpr (DMA) {
-    kd.init(ks, htid);
-    vd.init(vs, htid);
-  } else {
-    kt.init(ks, htid);
-    vt.init(vs, htid);
-  }
-  const int nh0 = (ntiles + 1) / 2;
-  const int my_first = khalf == 0 ? 0 : nh0;
-  const int my_count = khalf == 0 ? nh0 : ntiles - nh0;
-  S* const hsmem = smem + khalf * C::HALF;
-  const uint32_t lds0 = lds_addr(hsmem);
-  auto load_stage = [&](int n0, int st) {
-    const int rows = min(C::BN, sk - n0);
-    if constexpr (DMA) {
-      const uint32_t base = lds0 + (uint32_t)(st * C::STAGE) * 2u;
-      kd.load(rows_rsrc_words<D>(kbase + (int64_t)n0 * ks, ks, rows), base, wave);
-      vd.load(rows_rsrc_words<D>(vbase + (int64_t)n0 * vs, vs, rows), base + C::KT * 2u, wave);
-    } else {
-      kt.load(rows_rsrc<D>(kbase + (int64_t)n0 * ks, ks, rows));
-      vt.load(rows_rsrc<D>(vbase + (int64_t)n0 * vs, vs, rows));
-    }
-  };
-  auto store_stage = [&](int st) {
-    if constexpr (!DMA) {
-      S* base = hsmem + st * C::STAGE;
-      kt.store(base, htid);
-      vt.store(base + C::KT, htid);
-    }
-  };
-
-  const VisBounds qvb = row_block_bounds(md, m0w, mrows);
-  if (my_count > 0) {
-    load_stage(lo + my_first * C::BN, 0);
-    store_stage(0);
-  }
   wait_vm_all();
   __syncthreads();
   for (int t = 0; t < nh0; ++t) {

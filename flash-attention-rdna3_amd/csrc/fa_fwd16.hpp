@@ -109,16 +109,6 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
   const bool mvalid = m < sq;
 
   s16x8 qop[C::NSTEP];
-  {
-    const S* qrow = qb + (int64_t)(mvalid ? m : 0) * qs + 8 * h;
-#pragma unroll
-    for (int s = 0; s < C::NSTEP; ++s) qop[s] = load_op<Tag>(qrow + 16 * s);
-    if (!mvalid) {
-#pragma unroll
-      for (int s = 0; s < C::NSTEP; ++s) qop[s] = zero_op<Tag>();
-    }
-    wait_vm_all();
-  }
 
   float m_i = kNegInf, l_i = 0.f;
   f32x16 acc[C::NDB];
@@ -152,8 +142,18 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
   };
   const VisBounds vbnd = row_block_bounds(md, m0w, mrows);
 
+  // The first tiles' DMA and the Q loads share one round trip to memory.
   if (my_count > 0) load_tiles(0);
-  wait_vm_all();
+  {
+    const S* qrow = qb + (int64_t)(mvalid ? m : 0) * qs + 8 * h;
+#pragma unroll
+    for (int s = 0; s < C::NSTEP; ++s) qop[s] = load_op<Tag>(qrow + 16 * s);
+    wait_vm_all();
+    if (!mvalid) {
+#pragma unroll
+      for (int s = 0; s < C::NSTEP; ++s) qop[s] = zero_op<Tag>();
+    }
+  }
   __syncthreads();
 
   for (int t = 0; t < nh0; ++t) {
