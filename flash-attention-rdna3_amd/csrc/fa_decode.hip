@@ -318,15 +318,18 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
 
 template <typename Tag, int D, bool PAGED>
 static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
-  // Paged caches with blocks under 16 keys take the generic kernel (their
-  // per-row page lookups would enter the streaming kernel's vmcnt sequence).
+  // Paged caches with blocks under 4 keys take the generic kernel (a chunk
+  // would need more page ids than the streaming kernel keeps in scalars).
   if constexpr (D <= 128) {
-    if (!PAGED || a.block_shift >= 4) {
+    if (!PAGED || a.block_shift >= 2) {
       using C = Dec2Cfg<D>;
       const int group = a.heads_q / a.heads_kv;
       const int nrb = (group * a.seqlen_q + 15) / 16;
       dim3 grid(a.heads_kv * nrb * a.num_splits, a.batch);
-      auto kern = a.kv8 ? decode2_kernel<Tag, D, PAGED ? 1 : 0, true> : decode2_kernel<Tag, D, PAGED ? 1 : 0>;
+      constexpr int PG1 = PAGED ? 1 : 0, PG2 = PAGED ? 2 : 0;
+      const bool small = PAGED && a.block_shift < 4;
+      auto kern = a.kv8 ? (small ? decode2_kernel<Tag, D, PG2, true> : decode2_kernel<Tag, D, PG1, true>)
+                        : (small ? decode2_kernel<Tag, D, PG2> : decode2_kernel<Tag, D, PG1>);
       hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(kern, grid, dim3(C::NT), C::LDS_BYTES, stream, a);

@@ -74,7 +74,8 @@ struct Dec2Cfg {
 };
 
 // PAGE: 0 contiguous cache; 1 paged with block_size >= 16 (a 32-key chunk
-// spans at most two pages, whose ids are wave-uniform scalar loads).
+// spans at most two pages, whose ids are wave-uniform scalar loads); 2 paged
+// with block_size 4 or 8 (up to eight pages per chunk, one id per 4 keys).
 //
 // Pipeline: each wave owns NBUF chunk slots of registers.  Slot j holds chunk
 // k = NBUF*i + j: K in the MFMA A layout (lane row l%16, 8 dims per k-step)
@@ -89,7 +90,7 @@ struct Dec2Cfg {
 // KV8: the cache holds fp8 (OCP e4m3) K and V.
 template <typename Tag, int D, int PAGE, bool KV8 = false>
 __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
-  static_assert(PAGE == 0 || PAGE == 1, "decode2 handles contiguous and >=16-key pages");
+  static_assert(PAGE >= 0 && PAGE <= 2, "decode2 handles contiguous caches and pages of >= 4 keys");
   constexpr bool PAGED = PAGE != 0;
   using C = Dec2Cfg<D, KV8>;
   using EL = Elem<Tag>;
@@ -175,15 +176,31 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
     pg0 = btab[bt_row + (int64_t)min(n0 >> a.block_shift, last) * a.bt_stride[1]];
     pg1 = btab[bt_row + (int64_t)min((n0 + 16) >> a.block_shift, last) * a.bt_stride[1]];
   };
+  // PAGE 2: ids of the pages holding rows [4i, 4i + 4) of a chunk.
+  struct Pages8 { int p0, p1, p2, p3, p4, p5, p6, p7; };
+  auto chunk_pages8 = [&](int c, Pages8& pg) {
+    const int n0 = c * C::CK;
+    const int last = (a.max_len - 1) >> a.block_shift;
+    auto id = [&](int i) { return btab[bt_row + (int64_t)min((n0 + 4 * i) >> a.block_shift, last) * a.bt_stride[1]]; };
+    pg = Pages8{id(0), id(1), id(2), id(3), id(4), id(5), id(6), id(7)};
+  };
+  // The page of chunk row r (a per-lane choice among uniform ids, as selects).
+  auto page8 = [&](const Pages8& pg, int r) -> int {
+    const int g = r >> 2;
+    const int p01 = (g & 1) ? pg.p1 : pg.p0, p23 = (g & 1) ? pg.p3 : pg.p2;
+    const int p45 = (g & 1) ? pg.p5 : pg.p4, p67 = (g & 1) ? pg.p7 : pg.p6;
+    const int p03 = (g & 2) ? p23 : p01, p47 = (g & 2) ? p67 : p45;
+    return (g & 4) ? p47 : p03;
+  };
   // Element offset of key n's row from the per-(b, hk) base, or -1 if absent
   // (branch-free).
-  auto key_off = [&](int n, int pg0, int pg1, const int64_t* st) -> int64_t {
+  auto key_off = [&](int n, int pg0, int pg1, const Pages8& p8, const int64_t* st) -> int64_t {
     bool ok = n < len;
     int64_t off;
     if constexpr (PAGE == 0) {
       off = (int64_t)n * st[2];
     } else {
-      const int phys = ((n & 31) < 16) ? pg0 : pg1;
+      const int phys = PAGE == 2 ? page8(p8, n & 31) : ((n & 31) < 16) ? pg0 : pg1;
       ok = ok && phys >= 0 && phys < a.num_blocks;
       off = (int64_t)phys * st[0] + (int64_t)(n & bs_mask) * st[1];
     }
@@ -197,10 +214,12 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
   auto issue_chunk = [&](int c, bool live, KRaw (&kd)[2][C::KN], VRaw (&vd)[C::VN]) {
     const int n0 = c * C::CK;
     int pg0 = 0, pg1 = 0;
+    Pages8 p8{};
     if constexpr (PAGE == 1) chunk_pages(c, pg0, pg1);
+    if constexpr (PAGE == 2) chunk_pages8(c, p8);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      int64_t ko = key_off(n0 + 16 * kb + l16, pg0, pg1, a.k_stride);
+      int64_t ko = key_off(n0 + 16 * kb + l16, pg0, pg1, p8, a.k_stride);
       ko = (ko < 0 || !live) ? 0 : ko;
 #pragma unroll
       for (int s = 0; s < C::KN; ++s) {
@@ -215,7 +234,7 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
     for (int i = 0; i < C::VN; ++i) {
       const int slot = 64 * i + lane;
       const int row = slot / PPR;
-      int64_t vo = key_off(n0 + row, pg0, pg1, a.v_stride);
+      int64_t vo = key_off(n0 + row, pg0, pg1, p8, a.v_stride);
       vo = (vo < 0 || !live) ? 0 : vo;
       vd[i] = *reinterpret_cast<const VRaw*>(vbase + vo + (slot % PPR) * (KV8 ? 16 : 8));
     }
@@ -223,9 +242,11 @@ __global__ __launch_bounds__(256) void decode2_kernel(DecodeArgs a) {
   // Bit k of the result: key n0 + k of the chunk is visible.
   auto chunk_mask = [&](int c) -> uint32_t {
     int pg0 = 0, pg1 = 0;
+    Pages8 p8{};
     if constexpr (PAGE == 1) chunk_pages(c, pg0, pg1);
+    if constexpr (PAGE == 2) chunk_pages8(c, p8);
     const int n = c * C::CK + (lane & 31);
-    const bool ok = key_off(n, pg0, pg1, a.k_stride) >= 0;
+    const bool ok = key_off(n, pg0, pg1, p8, a.k_stride) >= 0;
     return (uint32_t)__builtin_amdgcn_ballot_w64(ok && lane < 32);
   };
 

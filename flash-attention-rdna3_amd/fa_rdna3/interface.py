@@ -840,7 +840,7 @@ def _paged_launch(query, k_cache, v_cache, block_table, context_lens, softmax_sc
     softmax_scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
 
     kdim = _kernel_head_dim(head_dim)
-    if num_splits is None and kdim <= 128 and block_size >= 16:
+    if num_splits is None and kdim <= 128 and block_size >= 4:
         max_keys = block_table.shape[1] * block_size
         if max_context_len is not None:
             max_keys = min(max_keys, max_context_len)
