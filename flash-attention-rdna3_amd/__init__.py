@@ -15,7 +15,8 @@ if __package__:
 else:
     _here = os.path.dirname(os.path.abspath(__file__))
     _loaded = sys.modules.get("fa_rdna3")
-    if _loaded is not None and not os.path.abspath(_loaded.__file__).startswith(_here + os.sep):
+    _loaded_file = getattr(_loaded, "__file__", None) if _loaded is not None else None
+    if _loaded is not None and not (_loaded_file and os.path.abspath(_loaded_file).startswith(_here + os.sep)):
         raise RuntimeError("A different fa_rdna3 package is already loaded; restart ComfyUI "
                            "before loading this custom node")
     if _here not in sys.path:
