@@ -322,18 +322,21 @@ static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
   // would need more page ids than the streaming kernel keeps in scalars).
   if constexpr (D <= 128) {
     if (!PAGED || a.block_shift >= 2) {
-      using C = Dec2Cfg<D>;
       const int group = a.heads_q / a.heads_kv;
       const int nrb = (group * a.seqlen_q + 15) / 16;
       dim3 grid(a.heads_kv * nrb * a.num_splits, a.batch);
       constexpr int PG1 = PAGED ? 1 : 0, PG2 = PAGED ? 2 : 0;
       const bool small = PAGED && a.block_shift < 4;
-      auto kern = a.kv8 ? (small ? decode2_kernel<Tag, D, PG2, true> : decode2_kernel<Tag, D, PG1, true>)
-                        : (small ? decode2_kernel<Tag, D, PG2> : decode2_kernel<Tag, D, PG1>);
-      hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
-      if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(kern, grid, dim3(C::NT), C::LDS_BYTES, stream, a);
-      e = hipGetLastError();
+      auto launch2 = [&](auto kv8_t) -> hipError_t {
+        constexpr bool K8 = decltype(kv8_t)::value;
+        using C = Dec2Cfg<D, K8>;
+        auto kern = small ? decode2_kernel<Tag, D, PG2, K8> : decode2_kernel<Tag, D, PG1, K8>;
+        hipError_t err = allow_lds((const void*)kern, C::LDS_BYTES);
+        if (err != hipSuccess) return err;
+        hipLaunchKernelGGL(kern, grid, dim3(C::NT), C::LDS_BYTES, stream, a);
+        return hipGetLastError();
+      };
+      hipError_t e = a.kv8 ? launch2(std::true_type{}) : launch2(std::false_type{});
       if (e != hipSuccess || a.num_splits == 1) return e;
       const int rows = a.batch * a.heads_q * a.seqlen_q;
       hipLaunchKernelGGL((decode_combine2_kernel<Tag, D>), dim3((rows + 3) / 4), dim3(256), 0, stream, a);
