@@ -327,16 +327,20 @@ static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
       dim3 grid(a.heads_kv * nrb * a.num_splits, a.batch);
       constexpr int PG1 = PAGED ? 1 : 0, PG2 = PAGED ? 2 : 0;
       const bool small = PAGED && a.block_shift < 4;
-      auto launch2 = [&](auto kv8_t) -> hipError_t {
+      auto launch2 = [&](auto kv8_t, auto pg_t) -> hipError_t {
         constexpr bool K8 = decltype(kv8_t)::value;
-        using C = Dec2Cfg<D, K8>;
-        auto kern = small ? decode2_kernel<Tag, D, PG2, K8> : decode2_kernel<Tag, D, PG1, K8>;
+        constexpr int PG = decltype(pg_t)::value;
+        using C = Dec2Cfg<D, K8, PG == 2>;
+        auto kern = decode2_kernel<Tag, D, PG, K8>;
         hipError_t err = allow_lds((const void*)kern, C::LDS_BYTES);
         if (err != hipSuccess) return err;
         hipLaunchKernelGGL(kern, grid, dim3(C::NT), C::LDS_BYTES, stream, a);
         return hipGetLastError();
       };
-      hipError_t e = a.kv8 ? launch2(std::true_type{}) : launch2(std::false_type{});
+      using P1 = std::integral_constant<int, PG1>;
+      using P2 = std::integral_constant<int, PG2>;
+      hipError_t e = a.kv8 ? (small ? launch2(std::true_type{}, P2{}) : launch2(std::true_type{}, P1{}))
+                           : (small ? launch2(std::false_type{}, P2{}) : launch2(std::false_type{}, P1{}));
       if (e != hipSuccess || a.num_splits == 1) return e;
       const int rows = a.batch * a.heads_q * a.seqlen_q;
       hipLaunchKernelGGL((decode_combine2_kernel<Tag, D>), dim3((rows + 3) / 4), dim3(256), 0, stream, a);

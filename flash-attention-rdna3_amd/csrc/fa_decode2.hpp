@@ -20,14 +20,12 @@
 #include "fa_internal.hpp"
 #include "fa_tiles.hpp"
 
-// Waves per workgroup of the fp8-cache decode kernel: 8 (two per SIMD, two
-// chunk slots each).  An fp8 chunk is half the bytes of a 16-bit one, so the
-// per-chunk work, not the bytes in flight, bounds it; a second wave per SIMD
-// overlaps that work (measured 8-10 % faster than 4 waves with 4 slots).
-#ifndef FA_DEC8_NW
-#define FA_DEC8_NW 8
-#endif
-
+// Workgroups of 8 waves (two per SIMD, a smaller chunk-slot budget each) for
+// fp8 caches and for 4- / 8-key pages: there the per-chunk work (fp8
+// conversion, per-lane page choice), not the bytes in flight, bounds the
+// kernel, and a second wave per SIMD overlaps it (measured 8-10 % faster for
+// fp8, 7-14 % for small pages; 4 waves stay faster for 16-bit caches in
+// pages of >= 16 keys or contiguous).
 namespace fa {
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
@@ -47,9 +45,10 @@ __device__ inline void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
-template <int D, bool KV8 = false>
+template <int D, bool KV8 = false, bool SMALLPG = false>
 struct Dec2Cfg {
-  static constexpr int NW = KV8 ? FA_DEC8_NW : 4;
+  static constexpr bool WIDE = KV8 || SMALLPG;       // 8 waves, 64-VGPR slot budget
+  static constexpr int NW = WIDE ? 8 : 4;
   static constexpr int NT = 64 * NW;
   static constexpr int CK = 32;                      // keys per chunk
   static constexpr int CPR = D / 8;                  // 16-byte chunks per row
@@ -73,7 +72,7 @@ struct Dec2Cfg {
 #ifndef FA_DEC_SLOT_VGPRS8
 #define FA_DEC_SLOT_VGPRS8 64
 #endif
-  static constexpr int NBUF = (KV8 ? FA_DEC_SLOT_VGPRS8 : FA_DEC_SLOT_VGPRS) / SLOT_REGS;
+  static constexpr int NBUF = (KV8 ? FA_DEC_SLOT_VGPRS8 : WIDE ? 64 : FA_DEC_SLOT_VGPRS) / SLOT_REGS;
   static constexpr int WAVE_ELEMS = TILE;            // one private V tile per wave
   static constexpr int LOOP_BYTES = NW * WAVE_ELEMS * 2;
   static constexpr int OLD = 17;                     // merge buffer row stride (floats)
@@ -97,10 +96,10 @@ struct Dec2Cfg {
 // in this loop makes it drain every load at the loop head instead.)
 // KV8: the cache holds fp8 (OCP e4m3) K and V.
 template <typename Tag, int D, int PAGE, bool KV8 = false>
-__global__ __launch_bounds__(KV8 ? 64 * FA_DEC8_NW : 256) void decode2_kernel(DecodeArgs a) {
+__global__ __launch_bounds__((KV8 || PAGE == 2) ? 512 : 256) void decode2_kernel(DecodeArgs a) {
   static_assert(PAGE >= 0 && PAGE <= 2, "decode2 handles contiguous caches and pages of >= 4 keys");
   constexpr bool PAGED = PAGE != 0;
-  using C = Dec2Cfg<D, KV8>;
+  using C = Dec2Cfg<D, KV8, PAGE == 2>;
   using EL = Elem<Tag>;
   using S = uint16_t;
   using KE = typename std::conditional<KV8, uint8_t, S>::type;  // cache element
