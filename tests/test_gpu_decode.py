@@ -174,11 +174,13 @@ def test_paged_context_clamped_to_table_capacity():
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_paged_equals_contiguous_decode(dtype):
+@pytest.mark.parametrize("P", [16, 8, 4])
+def test_paged_equals_contiguous_decode(dtype, P):
     """Scattering a contiguous cache into random pages must not change the
-    answer beyond output rounding."""
+    answer beyond output rounding (pages of 16 keys and of 4 / 8 keys take
+    two page-lookup variants of the streaming kernel)."""
     torch.manual_seed(77)
-    B, Hq, Hkv, D, S, P = 3, 16, 4, 128, 3000, 16
+    B, Hq, Hkv, D, S = 3, 16, 4, 128, 3000
     q = torch.randn(B, Hq, 1, D, device=DEVICE, dtype=dtype)
     k = torch.randn(B, Hkv, S, D, device=DEVICE, dtype=dtype)
     v = torch.randn_like(k)
