@@ -21,8 +21,8 @@ Each function names the reference code it restates
   to the tensor (varlen.py:21-27).
 * ``decode`` - kernels/decode.py:9-125 (non-causal attention of a few query
   rows over a cache), plus the ``cache_seqlens`` key limit of this build.
-* ``kvcache_attention`` - no counterpart in the reference (the SURVEY's
-  first "next" row, the flash_attn_with_kvcache pattern of FlashAttention-2):
+* ``kvcache_attention`` - no counterpart in the reference (the
+  flash_attn_with_kvcache pattern of FlashAttention-2):
   new rows written into a copy of the cache at [len_b, len_b + Snew) below
   the cache size, then ``attention_forward`` of each sequence over its first
   len_b + Snew rows (bottom-right causal when asked).  Pinned by reduction to
@@ -30,8 +30,8 @@ Each function names the reference code it restates
   cache, causal), each checked against its own vectors.
 * ``paged_decode`` - kernels/paged.py:16-89: block-table gather, context
   clamped to table capacity, invalid physical ids contribute nothing.
-* ``paged_attention`` - no counterpart in the reference (the SURVEY's second
-  "next" row): ``paged_decode`` for Sq query rows per sequence, keys kept at
+* ``paged_attention`` - no counterpart in the reference (paged decode of
+  several query rows): ``paged_decode`` for Sq query rows per sequence, keys kept at
   their cache positions, bottom-right causal when asked.  Pinned by its
   reduction to ``paged_decode`` (Sq = 1) and to ``kvcache_attention`` over
   the gathered contiguous cache.
