@@ -312,6 +312,23 @@ def run_decode_configs(iters=50):
         res["paged_multi_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
                                      "frac_hbm": round(gb / PEAK_HBM_GBS, 4), "caches_flushed": "read of 512 MiB",
                                      "shape": "cfg4 cache, Sq = 4, causal"}
+        # Context for frac_hbm: what a plain library read of the same number
+        # of bytes reaches on this box (torch max-reduction, caches flushed).
+        # It is a reference point, not a ceiling: a hand-written streaming read
+        # does better.
+        ceil = {}
+        for name, nbytes in (("cfg3_bytes", cfg3_bytes(lens.tolist())), ("cfg4_bytes", cfg4_bytes())):
+            x = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+            for _ in range(3):
+                x.max()
+            tot = 0.0
+            for _ in range(iters):
+                _flush(flush)
+                tot += _event_time(lambda: x.max(), 1, stream)
+            ms = tot / iters
+            ceil[name] = {"bytes": nbytes, "us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+            del x
+        res["torch_read_reference"] = dict(ceil, how="torch int32 max-reduction over the same byte count, caches flushed")
     return res
 
 
