@@ -82,7 +82,6 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
     bounded_seq(f.cu_seqlens_k, b, f.total_k, k_start, sk);
   }
   const int n0 = nblk * C::BN;
-  FA_TRACE(0);
   if (n0 >= sk || num_n_blocks <= 0) return;
 
   const S* kbase = reinterpret_cast<const S*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1] +
@@ -324,7 +323,6 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
     }
   }
 
-  FA_TRACE(1);
   if (!nvalid) return;
   S* dkr = reinterpret_cast<S*>(p.dk) + b * p.dk_stride[0] + hk * p.dk_stride[1] +
            (int64_t)(k_start + n) * p.dk_stride[2];
@@ -394,7 +392,6 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
   const int b = bh / f.heads_q, hq = bh - b * f.heads_q;
   const int hk = hq / (f.heads_q / f.heads_kv);
   const int mblk = num_m_blocks - 1 - mb_rev;  // heaviest causal blocks first
-  FA_TRACE(0);
 
   int q_start = 0, sq = f.seqlen_q, k_start = 0, sk = f.seqlen_k;
   if (f.cu_seqlens_q) {
@@ -604,7 +601,6 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
     for (int db = 0; db < C::NDB; ++db) dq[db] += unpark_acc(ow + (wave * C::NDB + db) * 1024, lane);
   }
 
-  FA_TRACE(1);
   if (!mvalid) return;
   S* dqr = reinterpret_cast<S*>(p.dq) + b * p.dq_stride[0] + hq * p.dq_stride[1] +
            (int64_t)(q_start + m) * p.dq_stride[2];

@@ -312,30 +312,6 @@ __device__ inline void dispatch_mods(const Mods& md, F&& f) {
   else { if (al) with_bias(N{}, T{}); else with_bias(N{}, N{}); }
 }
 
-// Optional per-workgroup timeline for scheduling studies (build with
-// -DFA_TRACE_WG): thread 0 records start/end wall clock and its hardware
-// placement into a device array read back by fa_debug_trace_*().
-#ifdef FA_TRACE_WG
-static __device__ unsigned long long g_fa_trace[4 * 65536];
-__device__ inline void trace_wg(int slot) {
-  if (threadIdx.x != 0) return;
-  const unsigned id = blockIdx.x + blockIdx.y * gridDim.x;
-  if (id >= 65536) return;
-  volatile unsigned long long* e = g_fa_trace + 4 * id;
-  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
-  if (slot == 0) {
-    e[0] = t;
-    e[2] = __builtin_amdgcn_s_getreg((4) | (0 << 6) | (31 << 11));
-    e[3] = __builtin_amdgcn_s_getreg((20) | (0 << 6) | (15 << 11));
-  } else {
-    e[1] = t;
-  }
-}
-#define FA_TRACE(slot) trace_wg(slot)
-#else
-#define FA_TRACE(slot) ((void)0)
-#endif
-
 // Order of query blocks over the grid for kernels whose block cost grows with
 // the block index (causal attention): block slot `idx` of `nb` maps to the
 // heaviest half descending, then the lightest half ascending.  When the whole

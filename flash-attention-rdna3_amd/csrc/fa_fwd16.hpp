@@ -75,7 +75,6 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
   const int b = bh / p.heads_q, hq = bh - b * p.heads_q;
   const int hk = hq / (p.heads_q / p.heads_kv);
   const int mblk = num_m_blocks - 1 - mb_rev;  // heaviest causal blocks first
-  FA_TRACE(0);
 
   int q_start = 0, sq = p.seqlen_q, k_start = 0, sk = p.seqlen_k;
   if (p.cu_seqlens_q) {
@@ -319,7 +318,6 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
     m_i = mn;
   }
 
-  FA_TRACE(1);
   if (!mvalid) return;
   const float l_safe = (l_i == 0.f) ? 1.f : l_i;
   const float inv = 1.f / l_safe;

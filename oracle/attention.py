@@ -39,6 +39,14 @@ Each function names the reference code it restates
   interface.py:53-58, :61-77, :136-151.
 * ``split_combine`` - decode.py:79-125: LSE-weighted merge of split partials.
 
+Pins (tests/test_oracle.py, tests/test_refs_pin.py): torch float64
+autograd, central finite differences, closed forms, the committed golden
+vectors and the reference's known answers.  ``varlen_backward`` is pinned by
+torch float64 autograd of ragged packed cases, by finite differences of
+``varlen_forward`` (out-of-range cu_seqlens included) and by its reduction to
+``attention_backward``; ``attention_flops`` by known answers of the
+reference's bench convention.
+
 Dropout is not restated (its Philox bitstream is implementation-defined);
 tests check it statistically and by finite differences instead.
 """
@@ -194,6 +202,9 @@ def varlen_forward(q, k, v, cu_q, cu_k, causal=False, scale=None, window=(-1, -1
 
 def varlen_backward(q, k, v, dout, cu_q, cu_k, causal=False, scale=None, window=(-1, -1), softcap=0.0,
                     alibi=None):
+    """(dq, dk, dv) of sum(out * dout) for packed sequences: the dense
+    backward per bounded interval (varlen.py:186-421, dK/dV :193-317 and dQ
+    :325-421); rows of no sequence get zero gradient."""
     q, k, v, dout = _f64(q), _f64(k), _f64(v), _f64(dout)
     dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
     for (qs, lq), (ks, lk) in zip(bounded_intervals(cu_q, q.shape[0]), bounded_intervals(cu_k, k.shape[0])):

@@ -34,16 +34,17 @@ def attention(query, key, value, causal=False, scale=None, window=(-1, -1), soft
         key = key.repeat_interleave(group, dim=1)
         value = value.repeat_interleave(group, dim=1)
     scale = 1.0 / math.sqrt(query.shape[-1]) if scale is None else scale
-    logits = (torch.matmul(query, key.transpose(-1, -2)) * scale).float()
+    acc = torch.promote_types(query.dtype, torch.float32)  # fp32 softmax, fp64 kept for CPU pins
+    logits = (torch.matmul(query, key.transpose(-1, -2)) * scale).to(acc)
     sq, sk = logits.shape[-2:]
     if softcap > 0:
         logits = softcap * torch.tanh(logits / softcap)
     if bias is not None:
-        logits = logits + bias.float()
+        logits = logits + bias.to(acc)
     if alibi is not None:
         i = torch.arange(sq, device=logits.device)[:, None]
         j = torch.arange(sk, device=logits.device)[None, :]
-        logits = logits - alibi.float().view(1, -1, 1, 1) * (j - i - (sk - sq)).abs().float()
+        logits = logits - alibi.to(acc).view(1, -1, 1, 1) * (j - i - (sk - sq)).abs().to(acc)
     keep = keep_mask(sq, sk, causal, window, logits.device)
     logits = logits.masked_fill(~keep, float("-inf"))
     valid = torch.isfinite(logits).any(dim=-1, keepdim=True)

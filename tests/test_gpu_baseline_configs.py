@@ -77,14 +77,17 @@ def test_cfg5_varlen_window_softcap():
     fn = lambda a, b, c: flash_attention_varlen(a, b, c, cu, cu, mx, mx, causal=True, window_size=(1024, -1),
                                                 softcap=50.0)
     out = fn(q, k, v)
-    # Reference on a few sequences (full fp32 reference of all 16 is large).
+    # Every sequence against fp32 math attention, max-abs 1e-2 (bf16).
     starts = [0] + list(np.cumsum(lengths))
-    for i in (0, 3, 13, 14):
+    for i in range(len(lengths)):
         s, n = starts[i], lengths[i]
         ref = varlen_attention(q[s:s + n].float(), k[s:s + n].float(), v[s:s + n].float(), [n], [n], **kw)
-        assert max_err(out[s:s + n], ref) <= 1e-2
-    sel = [13, 3]  # short and mid sequences for the gradient check
-    for i in sel:
+        err = max_err(out[s:s + n], ref)
+        assert err <= 1e-2, (i, n, err)
+    # Gradients: sequences 14 and 0 (2023 and 1937 tokens) are longer than the
+    # 1024-key window, so the window bites; 13 and 3 are shorter than it.
+    assert lengths[14] > 1024 and lengths[0] > 1024 and lengths[13] < 1024
+    for i in (14, 0, 13, 3):
         s, n = starts[i], lengths[i]
         cu1 = torch.tensor([0, n], device=DEVICE, dtype=torch.int32)
         f1 = lambda a, b, c: flash_attention_varlen(a, b, c, cu1, cu1, n, n, causal=True,
@@ -96,12 +99,17 @@ def test_cfg5_varlen_window_softcap():
         naive = grads(r1, sl(q), sl(k), sl(v), sl(do))
         for kg, ng, eg, name in zip(kernel, naive, exact, ("dq", "dk", "dv")):
             assert_ratio(kg, ng, eg, 1e-3, name)
+            # absolute bound: bf16 output tolerance scaled by the gradient's size
+            err, scale = max_err(kg, eg), max(1.0, eg.abs().max().item())
+            print(f"cfg5 seq {i} ({n}) {name}: err {err:.3e} max|g| {scale:.3e}", flush=True)
+            assert err <= 1e-2 * scale, (i, name, err, scale)
     # Packed backward equals per-sequence backward (sequences are independent).
     full = grads(fn, q, k, v, do)
-    s, n = starts[3], lengths[3]
-    cu1 = torch.tensor([0, n], device=DEVICE, dtype=torch.int32)
-    one = grads(lambda a, b, c: flash_attention_varlen(a, b, c, cu1, cu1, n, n, causal=True,
-                                                       window_size=(1024, -1), softcap=50.0),
-                q[s:s + n], k[s:s + n], v[s:s + n], do[s:s + n])
-    for a, b in zip(full, one):
-        torch.testing.assert_close(a[s:s + n], b, atol=0, rtol=0)
+    for i in (3, 14):
+        s, n = starts[i], lengths[i]
+        cu1 = torch.tensor([0, n], device=DEVICE, dtype=torch.int32)
+        one = grads(lambda a, b, c: flash_attention_varlen(a, b, c, cu1, cu1, n, n, causal=True,
+                                                           window_size=(1024, -1), softcap=50.0),
+                    q[s:s + n], k[s:s + n], v[s:s + n], do[s:s + n])
+        for a, b in zip(full, one):
+            torch.testing.assert_close(a[s:s + n], b, atol=0, rtol=0)

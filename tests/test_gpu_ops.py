@@ -5,6 +5,7 @@ test_torch_library.py, test_tiny.py, test_dropout.py, test_sdpa_dispatch.py)."""
 import math
 import threading
 
+import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
@@ -13,6 +14,7 @@ import fa_rdna3.sdpa as sdpa_mod
 from fa_rdna3 import (disable_rdna3_flash_attention, enable_rdna3_flash_attention, flash_attention,
                       use_rdna3_flash_attention)
 from fa_rdna3.interface import _backward, _can_use_tiny_forward, _forward
+from oracle import attention as oracle
 
 pytestmark = pytest.mark.gpu
 DEVICE = "cuda"
@@ -50,16 +52,10 @@ def _packed(seq):
     return tuple(t.transpose(1, 2) for t in packed.unbind(2))
 
 
-def _tiny_ref(q, k, v, bias=None):
-    s = torch.matmul(q, k.transpose(-1, -2)) / math.sqrt(HEAD_DIM)
-    if bias is not None:
-        s = s + bias
-    return torch.matmul(torch.softmax(s, dim=-1).nan_to_num(), v)
-
-
 @pytest.mark.parametrize("seq", [1, 6, 19, 32])
 @pytest.mark.parametrize("bias_kind", ["none", "broadcast", "full", "masked_row"])
 def test_tiny_fp32(seq, bias_kind):
+    """The fp32 tiny path (reference interface.py:84-104) against the oracle."""
     torch.manual_seed(seq)
     q, k, v = _packed(seq)
     bias = None
@@ -70,7 +66,9 @@ def test_tiny_fp32(seq, bias_kind):
         if bias_kind == "masked_row":
             bias[:, :, seq // 2, :] = float("-inf")
     out = flash_attention(q, k, v, bias=bias)
-    assert (out - _tiny_ref(q, k, v, bias)).abs().max().item() < 2e-6
+    np_ = lambda t: None if t is None else t.double().cpu().numpy()
+    ref, _ = oracle.attention_forward(np_(q), np_(k), np_(v), bias=np_(bias))
+    assert np.abs(out.double().cpu().numpy() - ref).max() < 2e-6
 
 
 @pytest.mark.parametrize("has_bias", [False, True])

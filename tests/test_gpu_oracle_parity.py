@@ -82,3 +82,48 @@ def test_varlen_vs_oracle():
     ref, _ = oracle.varlen_forward(q.float().numpy(), k.float().numpy(), v.float().numpy(), cu.numpy(), cu.numpy(),
                                    causal=True, window=(30, -1), softcap=15.0)
     assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-3
+
+
+VARLEN_MODS = [
+    dict(causal=False, window=(-1, -1), softcap=0.0, alibi=False),
+    dict(causal=True, window=(-1, -1), softcap=0.0, alibi=False),
+    dict(causal=True, window=(31, 0), softcap=0.0, alibi=False),
+    dict(causal=False, window=(-1, -1), softcap=30.0, alibi=False),
+    dict(causal=True, window=(-1, -1), softcap=0.0, alibi=True),
+    dict(causal=True, window=(100, -1), softcap=50.0, alibi=False),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("mi", range(len(VARLEN_MODS)))
+@pytest.mark.parametrize("cross", [False, True])
+def test_varlen_backward_vs_oracle(dtype, mi, cross):
+    """Packed dQ/dK/dV (reference kernels/varlen.py:186-421, cases of
+    tests/test_varlen_mods.py:17-43) against oracle.varlen_backward."""
+    m = VARLEN_MODS[mi]
+    g = torch.Generator().manual_seed(100 + mi * 2 + int(cross))
+    lq = [1, 77, 200, 33, 130]
+    lk = [5, 60, 200, 129, 1] if cross else lq
+    cu_q = torch.tensor([0] + list(np.cumsum(lq)), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(np.cumsum(lk)), dtype=torch.int32)
+    hq, hk, d = 4, 2, 64
+    q = torch.randn(sum(lq), hq, d, generator=g).to(dtype)
+    k = torch.randn(sum(lk), hk, d, generator=g).to(dtype)
+    v = torch.randn(sum(lk), hk, d, generator=g).to(dtype)
+    do = torch.randn(sum(lq), hq, d, generator=g).to(dtype)
+    slopes = alibi_slopes(hq, device="cpu") if m["alibi"] else None
+    tq, tk, tv = (t.to(DEVICE).requires_grad_(True) for t in (q, k, v))
+    out = flash_attention_varlen(tq, tk, tv, cu_q.to(DEVICE), cu_k.to(DEVICE), max(lq), max(lk),
+                                 causal=m["causal"], window_size=m["window"], softcap=m["softcap"],
+                                 alibi_slopes=None if slopes is None else slopes.to(DEVICE))
+    out.backward(do.to(DEVICE))
+    np_ = lambda t: None if t is None else t.float().numpy()
+    args = (cu_q.numpy(), cu_k.numpy(), m["causal"], None, m["window"], m["softcap"], np_(slopes))
+    ref_o, _ = oracle.varlen_forward(np_(q), np_(k), np_(v), *args)
+    otol = TOL[dtype][0]
+    assert np.abs(out.detach().float().cpu().numpy() - ref_o).max() <= otol
+    rg = oracle.varlen_backward(np_(q), np_(k), np_(v), np_(do), *args)
+    tol = 2e-2 if dtype == torch.float16 else 1.5e-1
+    for got, want, name in zip((tq.grad, tk.grad, tv.grad), rg, "qkv"):
+        err = np.abs(got.float().cpu().numpy() - want).max()
+        assert err <= tol * max(1.0, np.abs(want).max()), (name, err)
