@@ -313,6 +313,31 @@ def run_decode_configs(iters=50):
         res["paged_multi_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1),
                                      "frac_hbm": round(gb / PEAK_HBM_GBS, 4), "caches_flushed": "read of 512 MiB",
                                      "shape": "cfg4 cache, Sq = 4, causal"}
+        del q4
+        # A ragged serving batch: 16 sequences from 64 to 32768 keys in one
+        # contiguous cache (GQA 32/8, D 128).  The split kernel shares its
+        # workgroups out by sequence length, so the long sequences do not
+        # leave the CUs of the short ones idle.
+        rl = [32768, 512, 1024, 300, 2048, 128, 4096, 700, 16384, 64, 900, 1500, 256, 8000, 100, 3000]
+        gr = _gen(3)
+        qr = torch.randn(16, 32, 1, 128, generator=gr).half().cuda()
+        kr = torch.randn(16, 8, 32768, 128, dtype=torch.float16, device="cuda")
+        vr = torch.randn_like(kr)
+        lr = torch.tensor(rl, dtype=torch.int32, device="cuda")
+        fr = lambda: flash_attention_decode(qr, kr, vr, cache_seqlens=lr)
+        for _ in range(5):
+            fr()
+        tot = 0.0
+        for _ in range(iters):
+            _flush(flush)
+            tot += _event_time(fr, 1, stream)
+        ms = tot / iters
+        br = sum(rl) * 8 * 128 * 2 * 2 + 2 * 16 * 32 * 128 * 2
+        gb = br / (ms * 1e-3) / 1e9
+        res["ragged_decode"] = {"us": round(ms * 1e3, 2), "GB/s": round(gb, 1), "frac_hbm": round(gb / PEAK_HBM_GBS, 4),
+                                "caches_flushed": "read of 512 MiB", "bytes": br,
+                                "shape": "B=16 lengths 64..32768 (sum 71780), Hq 32, Hkv 8, D 128, fp16"}
+        del qr, kr, vr
         # Context for frac_hbm: what a plain library read of the same number
         # of bytes reaches on this box (torch max-reduction, caches flushed).
         # It is a reference point, not a ceiling: a hand-written streaming read

@@ -111,6 +111,11 @@ size_t fa_params_size(int which) {
   return 0;
 }
 
+size_t fa_decode_ticket_count(int batch, int heads_q, int seqlen_q) {
+  if (batch <= 0 || heads_q <= 0 || seqlen_q <= 0) return 0;
+  return (size_t)batch * heads_q * seqlen_q;
+}
+
 size_t fa_decode_workspace_bytes(int batch, int heads_q, int seqlen_q, int head_dim, int num_splits) {
   if (batch <= 0 || heads_q <= 0 || seqlen_q <= 0 || head_dim <= 0 || num_splits <= 0) return 0;
   return fa::decode_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits);
@@ -160,6 +165,7 @@ int fa_decode_splitk(const fa_decode_params* params, void* stream) {
       !rows_ok(p.out, p.out_stride, 4, 2))
     return fail(FA_ERR_INVALID, "fa_decode_splitk: q/k/v/out need a unit last stride and 16-byte aligned rows");
   if (!p.workspace || !aligned16(p.workspace)) return fail(FA_ERR_INVALID, "fa_decode_splitk: workspace");
+  if ((reinterpret_cast<uintptr_t>(p.tickets) & 3u) != 0) return fail(FA_ERR_INVALID, "fa_decode_splitk: tickets");
   if (p.causal != 0 && p.causal != 1) return fail(FA_ERR_INVALID, "fa_decode_splitk: causal must be 0 or 1");
   return from_hip(fa::launch_decode(p, (hipStream_t)stream), "fa_decode_splitk");
 }
@@ -184,6 +190,7 @@ int fa_decode_paged(const fa_paged_params* params, void* stream) {
     return fail(FA_ERR_INVALID, "fa_decode_paged: q/caches/out need a unit last stride and 16-byte aligned rows");
   if (!p.block_table || !p.context_lens) return fail(FA_ERR_INVALID, "fa_decode_paged: metadata is NULL");
   if (!p.workspace || !aligned16(p.workspace)) return fail(FA_ERR_INVALID, "fa_decode_paged: workspace");
+  if ((reinterpret_cast<uintptr_t>(p.tickets) & 3u) != 0) return fail(FA_ERR_INVALID, "fa_decode_paged: tickets");
   return from_hip(fa::launch_paged(p, (hipStream_t)stream), "fa_decode_paged");
 }
 

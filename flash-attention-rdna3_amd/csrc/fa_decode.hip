@@ -55,6 +55,10 @@ struct DecodeArgs {
   float out_scale;      // multiplies the output (v_scale of an fp8 cache); 1 otherwise
   float* ws_o;          // [splits][B][Hq][Sq][D] fp32
   float* ws_lse;        // [splits][B][Hq][Sq] fp32
+  uint32_t* tickets;    // NULL: a second launch merges the splits; else per
+                        // (b, hk, row block) arrival counters, zero between calls
+  int32_t balanced;     // streaming kernel: share num_splits * batch workgroups
+                        // out over the sequences by length (needs tickets)
 };
 
 }  // namespace fa
@@ -86,8 +90,11 @@ struct DecCfg {
   static constexpr int NDB = DO / 32;
 };
 
+// Partial slots: num_splits per sequence, plus one per sequence for the
+// balanced partition (its per-sequence shares are rounded up to at least one
+// workgroup each).
 size_t decode_workspace_bytes(int batch, int heads_q, int seqlen_q, int head_dim, int num_splits) {
-  const size_t rows = (size_t)num_splits * batch * heads_q * seqlen_q;
+  const size_t rows = (size_t)(num_splits + 1) * batch * heads_q * seqlen_q;
   size_t bytes = rows * (size_t)head_dim * 4 + rows * 4;
   return (bytes + 255) / 256 * 256;
 }
@@ -317,14 +324,21 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
 }
 
 template <typename Tag, int D, bool PAGED>
-static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
+static hipError_t run_decode(DecodeArgs a, hipStream_t stream) {
   // Paged caches with blocks under 4 keys take the generic kernel (a chunk
   // would need more page ids than the streaming kernel keeps in scalars).
   if constexpr (D <= 128) {
     if (!PAGED || a.block_shift >= 2) {
       const int group = a.heads_q / a.heads_kv;
       const int nrb = (group * a.seqlen_q + 15) / 16;
-      dim3 grid(a.heads_kv * nrb * a.num_splits, a.batch);
+      // Balanced partition over all sequences when the merge is fused and the
+      // sequence lengths fit one wave's prefix scan.
+      // The in-launch merge addresses the workspace with 32-bit offsets.
+      if (decode_workspace_bytes(a.batch, a.heads_q, a.seqlen_q, D, a.num_splits) >= ((size_t)1 << 31))
+        a.tickets = nullptr;
+      a.balanced = (a.tickets != nullptr && a.batch <= 64) ? 1 : 0;
+      dim3 grid = a.balanced ? dim3(a.heads_kv * nrb * (a.num_splits + 1) * a.batch, 1)
+                             : dim3(a.heads_kv * nrb * a.num_splits, a.batch);
       constexpr int PG1 = PAGED ? 1 : 0, PG2 = PAGED ? 2 : 0;
       const bool small = PAGED && a.block_shift < 4;
       auto launch2 = [&](auto kv8_t, auto pg_t) -> hipError_t {
@@ -341,7 +355,7 @@ static hipError_t run_decode(const DecodeArgs& a, hipStream_t stream) {
       using P2 = std::integral_constant<int, PG2>;
       hipError_t e = a.kv8 ? (small ? launch2(std::true_type{}, P2{}) : launch2(std::true_type{}, P1{}))
                            : (small ? launch2(std::false_type{}, P2{}) : launch2(std::false_type{}, P1{}));
-      if (e != hipSuccess || a.num_splits == 1) return e;
+      if (e != hipSuccess || a.num_splits == 1 || a.tickets) return e;
       const int rows = a.batch * a.heads_q * a.seqlen_q;
       hipLaunchKernelGGL((decode_combine2_kernel<Tag, D>), dim3((rows + 3) / 4), dim3(256), 0, stream, a);
       return hipGetLastError();
@@ -382,7 +396,7 @@ static hipError_t decode_dispatch(int dtype, const DecodeArgs& a, hipStream_t s)
 }
 
 static void split_workspace(DecodeArgs& a, void* ws) {
-  const size_t rows = (size_t)a.num_splits * a.batch * a.heads_q * a.seqlen_q;
+  const size_t rows = (size_t)(a.num_splits + 1) * a.batch * a.heads_q * a.seqlen_q;
   a.ws_o = reinterpret_cast<float*>(ws);
   a.ws_lse = a.ws_o + rows * a.head_dim;
 }
@@ -412,6 +426,7 @@ hipError_t launch_decode(const fa_decode_params& p, hipStream_t s) {
   a.num_splits = p.num_splits;
   a.causal = p.causal ? 1 : 0;
   split_workspace(a, p.workspace);
+  a.tickets = p.tickets;
   return decode_dispatch<false>(p.dtype, a, s);
 }
 
@@ -445,6 +460,7 @@ hipError_t launch_paged(const fa_paged_params& p, hipStream_t s) {
   a.scale_log2 = p.softmax_scale * (a.kv8 ? p.k_scale : 1.f) * kLog2e;
   a.out_scale = a.kv8 ? p.v_scale : 1.f;
   split_workspace(a, p.workspace);
+  a.tickets = p.tickets;
   return decode_dispatch<true>(p.dtype, a, s);
 }
 

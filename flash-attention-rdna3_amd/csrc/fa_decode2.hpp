@@ -76,7 +76,7 @@ struct Dec2Cfg {
   static constexpr int WAVE_ELEMS = TILE;            // one private V tile per wave
   static constexpr int LOOP_BYTES = NW * WAVE_ELEMS * 2;
   static constexpr int OLD = 17;                     // merge buffer row stride (floats)
-  static constexpr int MERGE_BYTES = NW * D * OLD * 4 + 2 * NW * 16 * 4;
+  static constexpr int MERGE_BYTES = NW * D * OLD * 4 + 2 * NW * 16 * 4 + 16;  // + ticket flag
   static constexpr int LDS_BYTES = LOOP_BYTES > MERGE_BYTES ? LOOP_BYTES : MERGE_BYTES;
 };
 
@@ -113,7 +113,7 @@ __global__ __launch_bounds__((KV8 || PAGE == 2) ? 512 : 256) void decode2_kernel
   const int g4 = lane >> 4, l16 = lane & 15;
   const int group = a.heads_q / a.heads_kv;
   const int rows = group * a.seqlen_q;
-  // Grid (heads_kv * row blocks * num_splits, batch), KV heads fastest: the
+  // Grid (heads_kv * row blocks * slots, batch or 1), KV heads fastest: the
   // KV heads of one key range are adjacent in dispatch order, so a paged
   // cache's pages (all KV heads of a token row side by side) are read by
   // neighbouring workgroups at about the same time (measured 4 % faster on
@@ -121,16 +121,16 @@ __global__ __launch_bounds__((KV8 || PAGE == 2) ? 512 : 256) void decode2_kernel
   const int nrb = (rows + 15) / 16;
   const int hk = blockIdx.x % a.heads_kv;
   const int rb = (blockIdx.x / a.heads_kv) % nrb;
-  const int split = blockIdx.x / (a.heads_kv * nrb);
-  const int b = blockIdx.y;
-
-  int len = a.max_len;
-  if (a.lens) len = min(max(a.lens[b * a.lens_stride] + a.lens_add, 0), a.max_len);
-  const int nch = (len + C::CK - 1) / C::CK;
-  const int per = nch / a.num_splits, extra = nch % a.num_splits;
-  const int c0 = split * per + min(split, extra);
-  const int cnt = per + (split < extra ? 1 : 0);
-
+  const int slot = blockIdx.x / (a.heads_kv * nrb);
+  auto seq_len = [&](int bb) {
+    return a.lens ? min(max(a.lens[bb * a.lens_stride] + a.lens_add, 0), a.max_len) : a.max_len;
+  };
+  // One segment: chunks [c0, c0 + cnt) of sequence b.  With nctr == 1 the
+  // segment is the whole sequence and writes the output rows; otherwise it
+  // is one of nctr partials, stored at partial slot `pslot`, and the last of
+  // them to arrive merges slots pfirst + k * pstep, k < nctr.
+  auto segment = [&](const int b, const int len, const int c0, const int cnt, const int nctr, const int pslot,
+                     const int pfirst, const int pstep) {
   // This lane's packed query column (group head, query row).
   const int r = rb * 16 + l16;
   const bool rvalid = r < rows;
@@ -412,15 +412,175 @@ __global__ __launch_bounds__((KV8 || PAGE == 2) ? 512 : 256) void decode2_kernel
     o = o / Ls * a.out_scale;  // out_scale: v_scale of an fp8 cache, else 1
     const int gg = row / a.seqlen_q, mm = row - gg * a.seqlen_q;
     const int hh = hk * group + gg;
-    if (a.num_splits == 1) {
+    if (nctr == 1) {
       S* op = reinterpret_cast<S*>(a.out) + b * a.out_stride[0] + hh * a.out_stride[1] + mm * a.out_stride[2];
       op[d] = EL::from_f(o);
     } else {
-      const int64_t prow = (((int64_t)split * a.batch + b) * a.heads_q + hh) * a.seqlen_q + mm;
-      a.ws_o[prow * a.head_dim + d] = o;
-      if (d == 0) a.ws_lse[prow] = (M == kNegInf || L == 0.f) ? kNegInf : (M + __log2f(L)) * kLn2;
+      const int64_t prow = ((int64_t)pslot * a.heads_q + hh) * a.seqlen_q + mm;
+      const float lse = (M == kNegInf || L == 0.f) ? kNegInf : (M + __log2f(L)) * kLn2;
+      if (a.tickets) {
+        // Agent-scope stores are written through to the device's coherence
+        // point (the XCDs' L2s are not coherent with each other), so the
+        // merging workgroup, on any XCD, reads them with agent-scope loads.
+        __hip_atomic_store(a.ws_o + prow * a.head_dim + d, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) __hip_atomic_store(a.ws_lse + prow, lse, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        a.ws_o[prow * a.head_dim + d] = o;
+        if (d == 0) a.ws_lse[prow] = lse;
+      }
     }
   }
+  if (nctr == 1 || a.tickets == nullptr) return;
+
+  // Fused merge of the splits: every workgroup of this (batch, KV head, row
+  // block) publishes its partial and takes a ticket; the one that draws the
+  // last ticket resets it to zero for the next call and merges all partials
+  // in split order.  Publication: the partials above were stored at agent
+  // scope (write-through, acknowledged once visible device-wide), and each
+  // wave waits for those acknowledgements (vmcnt 0) before the barrier that
+  // precedes the ticket, so no L2 write-back or invalidate is needed (an
+  // agent-scope release / acquire fence pair costs about 20 us per call
+  // here).  No workgroup waits for another, so nothing can stall on a
+  // missing arrival.
+  wait_vm_all();
+  __syncthreads();
+  int* flag = reinterpret_cast<int*>(lw + C::NW * 16);
+  if (tid == 0) {
+    uint32_t* t = a.tickets + ((int64_t)b * a.heads_kv + hk) * nrb + rb;
+    const uint32_t prev = __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev == (uint32_t)(nctr - 1);
+    if (last) __hip_atomic_store(t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (*flag == 0) return;
+  // Merge: TPR threads per row, each owning DPT consecutive dims.  Per chunk
+  // of 8 contributors a thread issues all its loads at once (their LSEs and
+  // DPT-float pieces of their partial rows, agent-scope buffer loads), then
+  // folds them in contributor order with a running max (natural-log
+  // domain): one memory round trip per chunk.
+  constexpr int TPR = C::NT / 16;
+  constexpr int DPT = D / TPR;  // 8 / 4 / 2 / 1 floats
+  static_assert(DPT >= 1 && DPT * TPR == D, "merge layout");
+  constexpr int SC1 = 16;       // cache policy: agent scope (coherent across XCDs)
+  const int cc = tid / TPR, d0 = (tid % TPR) * DPT;
+  const int row = rb * 16 + cc;
+  if (row >= rows) return;
+  const int gg = row / a.seqlen_q, mm = row - gg * a.seqlen_q;
+  const int hh = hk * group + gg;
+  const int64_t plane = (int64_t)a.heads_q * a.seqlen_q;
+  const int64_t prow = (int64_t)hh * a.seqlen_q + mm;
+  const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(a.ws_lse, (short)0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(a.ws_o, (short)0, 0x7FFFFFFF, 0x00020000);
+  float M = kNegInf, den = 0.f, num[DPT];
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) num[e] = 0.f;
+  for (int k0 = 0; k0 < nctr; k0 += 8) {
+    float ls[8], part[8][DPT];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t srow = (int64_t)(pfirst + min(k0 + u, nctr - 1) * pstep) * plane + prow;
+      ls[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, (int)(srow * 4), 0, SC1));
+      const int off = (int)((srow * D + d0) * 4);
+      if constexpr (DPT >= 4) {
+#pragma unroll
+        for (int q = 0; q < DPT / 4; ++q) {
+          // (bit_cast the whole result: subscripting the builtin's vector
+          // directly compiles to one dword load splatted to all four.)
+          const f32x4v w = __builtin_bit_cast(f32x4v, __builtin_amdgcn_raw_buffer_load_b128(ro, off + 16 * q, 0, SC1));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) part[u][4 * q + e] = w[e];
+        }
+      } else if constexpr (DPT == 2) {
+        typedef float f32x2v __attribute__((ext_vector_type(2)));
+        const f32x2v w = __builtin_bit_cast(f32x2v, __builtin_amdgcn_raw_buffer_load_b64(ro, off, 0, SC1));
+        part[u][0] = w[0];
+        part[u][1] = w[1];
+      } else {
+        part[u][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, off, 0, SC1));
+      }
+    }
+    float mc = M;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) mc = fmaxf(mc, k0 + u < nctr ? ls[u] : kNegInf);
+    const float mu = (mc == kNegInf) ? 0.f : mc;
+    const float sc = (M == kNegInf) ? 0.f : __expf(M - mu);
+    den *= sc;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) num[e] *= sc;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float w = (k0 + u < nctr && ls[u] != kNegInf) ? __expf(ls[u] - mu) : 0.f;
+      den += w;
+#pragma unroll
+      for (int e = 0; e < DPT; ++e) num[e] += w * part[u][e];
+    }
+    M = mc;
+  }
+  const float inv = 1.f / (den == 0.f ? 1.f : den);
+  S* op = reinterpret_cast<S*>(a.out) + b * a.out_stride[0] + hh * a.out_stride[1] + mm * a.out_stride[2] + d0;
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) op[e] = EL::from_f(num[e] * inv);
+  };  // segment
+
+  // Which segment this workgroup runs.
+  int sb, slen, sc0, scnt, snctr, spslot, spfirst, spstep;
+  if (a.balanced) {
+    // Balanced: the workgroups of one (KV head, row block) are shared out
+    // over the sequences in proportion to their chunk counts, so a long
+    // sequence among short ones is split finely and the CUs of short
+    // sequences do not idle.  With G = num_splits * batch the target count,
+    // sequence b gets g_b = max(1, floor(n_b * G / T)) workgroups (T = total
+    // chunks; equal lengths give exactly num_splits each) and an even share
+    // of its chunks per workgroup.  The sum stays within G + batch, the
+    // workgroups launched per (KV head, row block); those past the last
+    // sequence's share exit.  Sequence b's partial slots are the
+    // consecutive workgroup slots [P_b, P_b + g_b).
+    const int G = a.num_splits * a.batch;
+    const int len_l = lane < a.batch ? seq_len(lane) : 0;
+    const int nch_l = (len_l + C::CK - 1) / C::CK;
+    int tot = nch_l;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    const int gb = lane < a.batch ? max(1, tot > 0 ? (int)((int64_t)nch_l * G / tot) : 0) : 0;
+    int incl = gb;  // inclusive prefix sum over lanes (sequences)
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o, 64);
+      incl += lane >= o ? y : 0;
+    }
+    // b = number of sequences whose share ends at or before this slot.
+    const int b = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < a.batch && incl <= slot));
+    if (b >= a.batch) return;
+    const int g_b = __builtin_amdgcn_readlane(gb, b);
+    const int p_b = __builtin_amdgcn_readlane(incl, b) - g_b;
+    const int n = __builtin_amdgcn_readlane(nch_l, b);
+    const int j = slot - p_b;
+    const int per = n / g_b, extra = n % g_b;
+    sb = b;
+    slen = __builtin_amdgcn_readlane(len_l, b);
+    sc0 = j * per + min(j, extra);
+    scnt = per + (j < extra ? 1 : 0);
+    snctr = g_b;
+    spslot = slot;
+    spfirst = p_b;
+    spstep = 1;
+  } else {
+    // Per sequence: split `slot` of sequence blockIdx.y takes an even share
+    // of its chunks; the partial slots of sequence b are s * batch + b.
+    const int b = blockIdx.y;
+    slen = seq_len(b);
+    const int nch = (slen + C::CK - 1) / C::CK;
+    const int per = nch / a.num_splits, extra = nch % a.num_splits;
+    sb = b;
+    sc0 = slot * per + min(slot, extra);
+    scnt = per + (slot < extra ? 1 : 0);
+    snctr = a.num_splits;
+    spslot = slot * a.batch + b;
+    spfirst = b;
+    spstep = a.batch;
+  }
+  segment(sb, slen, sc0, scnt, snctr, spslot, spfirst, spstep);
 }
 
 // One wave per output row: out = sum_s w_s O_s / sum_s w_s with

@@ -13,7 +13,7 @@ import threading
 
 import torch
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 DTYPE_CODE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
 _LIB_NAME = "libfa_mi355x.so"
@@ -68,7 +68,7 @@ class DecodeParams(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("causal", ctypes.c_int32), ("cache_seqlens_add", ctypes.c_int32),
         ("kv_fp8", ctypes.c_int32), ("k_scale", ctypes.c_float), ("v_scale", ctypes.c_float),
-        ("reserved0", ctypes.c_int32),
+        ("reserved0", ctypes.c_int32), ("tickets", ctypes.c_void_p),
     ]
 
 
@@ -100,6 +100,7 @@ class PagedParams(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("causal", ctypes.c_int32), ("kv_fp8", ctypes.c_int32),
         ("k_scale", ctypes.c_float), ("v_scale", ctypes.c_float),
+        ("tickets", ctypes.c_void_p),
     ]
 
 
@@ -118,6 +119,7 @@ class TinyParams(ctypes.Structure):
 _STRUCTS = (FwdParams, BwdParams, DecodeParams, PagedParams, TinyParams, AppendParams)
 EXPORTS = (
     "fa_abi_version", "fa_last_error_string", "fa_params_size", "fa_decode_workspace_bytes",
+    "fa_decode_ticket_count",
     "fa_fwd", "fa_bwd", "fa_bwd_phase", "fa_decode_splitk", "fa_decode_paged", "fa_tiny_fwd_f32",
     "fa_kvcache_append",
 )
@@ -150,6 +152,8 @@ def lib():
         handle.fa_params_size.argtypes = [ctypes.c_int]
         handle.fa_decode_workspace_bytes.restype = ctypes.c_size_t
         handle.fa_decode_workspace_bytes.argtypes = [ctypes.c_int] * 5
+        handle.fa_decode_ticket_count.restype = ctypes.c_size_t
+        handle.fa_decode_ticket_count.argtypes = [ctypes.c_int] * 3
         for name, struct in (("fa_fwd", FwdParams), ("fa_bwd", BwdParams),
                              ("fa_decode_splitk", DecodeParams), ("fa_decode_paged", PagedParams),
                              ("fa_tiny_fwd_f32", TinyParams), ("fa_kvcache_append", AppendParams)):
@@ -195,6 +199,34 @@ def call_bwd_phase(params, phase, device_tensor):
 
 def decode_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits):
     return int(lib().fa_decode_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits))
+
+
+# The split-K / paged decode merges its split partials inside the split
+# launch (last-arriving workgroup, arrival counters in `decode_tickets`).
+# False selects the two-launch path (split kernel, then a merge kernel).
+FUSED_SPLIT_MERGE = True
+
+_tickets = {}
+
+
+def decode_tickets(device_tensor, batch, heads_q, seqlen_q):
+    """Address of zeroed uint32 arrival counters for one decode call on the
+    current stream of the tensor's device, or None for the two-launch merge.
+
+    The decode kernels leave every counter at zero, so one buffer per
+    (device, stream) serves all calls issued in stream order; it grows when
+    a call needs more counters than it holds."""
+    if not FUSED_SPLIT_MERGE:
+        return None
+    need = int(lib().fa_decode_ticket_count(batch, heads_q, seqlen_q))
+    stream = torch.cuda.current_stream(device_tensor.device)
+    key = (device_tensor.device.index, stream.cuda_stream)
+    buf = _tickets.get(key)
+    if buf is None or buf.numel() < need:
+        size = max(need, 1024 if buf is None else 2 * buf.numel())
+        buf = torch.zeros(size, dtype=torch.int32, device=device_tensor.device)
+        _tickets[key] = buf
+    return buf.data_ptr()
 
 
 def kernel_ready(t):

@@ -575,6 +575,7 @@ def _decode_launch(query, key, value, softmax_scale, lens, causal, lens_add=0, f
     p.softmax_scale = softmax_scale
     p.num_splits = num_splits
     p.workspace = workspace.data_ptr()
+    p.tickets = _native.decode_tickets(query, batch, heads, seqlen_q)
     p.causal = 1 if causal else 0
     p.cache_seqlens_add = int(lens_add)
     if fp8_scales is not None:
@@ -879,6 +880,7 @@ def _paged_launch(query, k_cache, v_cache, block_table, context_lens, softmax_sc
         p.kv_fp8 = 1
         p.k_scale, p.v_scale = fp8_scales
     p.workspace = workspace.data_ptr()
+    p.tickets = _native.decode_tickets(query, batch, q_heads, seqlen_q)
     _native.call("fa_decode_paged", p, query)
     return out[..., :head_dim] if kdim != head_dim else out
 

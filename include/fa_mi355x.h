@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 2
+#define FA_ABI_VERSION 3
 
 typedef enum fa_dtype {
   FA_DTYPE_F16 = 0,
@@ -168,6 +168,13 @@ typedef struct fa_decode_params {
   float k_scale;
   float v_scale;
   int32_t reserved0;
+  uint32_t* tickets; /* NULL: the split partials are merged by a second launch.
+                        Else fa_decode_ticket_count(...) uint32 arrival counters,
+                        all zero before the call and left zero by it: the last
+                        split of each (batch, KV head, 16-row block) merges the
+                        partials in the same launch (head_dim <= 128 kernels;
+                        the others keep the second launch).  Calls that share
+                        one tickets array must not overlap in time. */
 } fa_decode_params;
 
 /*
@@ -247,6 +254,13 @@ typedef struct fa_paged_params {
                       0: they have `dtype` */
   float k_scale;
   float v_scale;
+  uint32_t* tickets; /* NULL: the split partials are merged by a second launch.
+                        Else fa_decode_ticket_count(...) uint32 arrival counters,
+                        all zero before the call and left zero by it: the last
+                        split of each (batch, KV head, 16-row block) merges the
+                        partials in the same launch (head_dim <= 128 kernels;
+                        the others keep the second launch).  Calls that share
+                        one tickets array must not overlap in time. */
 } fa_paged_params;
 
 /*
@@ -294,6 +308,9 @@ int fa_bwd(const fa_bwd_params* params, void* stream);
  * Triton calls, interface.py:226/:236/:258); it exists so profilers and
  * benchmarks can time each backward kernel on its own. */
 int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream);
+/* uint32 counters `tickets` needs: batch * heads_q * seqlen_q. */
+size_t fa_decode_ticket_count(int batch, int heads_q, int seqlen_q);
+
 int fa_decode_splitk(const fa_decode_params* params, void* stream);
 int fa_decode_paged(const fa_paged_params* params, void* stream);
 int fa_tiny_fwd_f32(const fa_tiny_params* params, void* stream);
