@@ -43,9 +43,12 @@ def test_abi_version_and_struct_layouts():
 
 
 def test_workspace_size():
-    # splits * B * H * Sq * (D + 1) fp32, rounded up to 256 bytes
+    # (splits + 1) * B * H * Sq * (D + 1) fp32, rounded up to 256 bytes: one
+    # partial slot per split and sequence, plus one per sequence for the
+    # length-proportional shares of the balanced partition
     n = _native.decode_workspace_bytes(4, 32, 1, 128, 8)
-    assert n == (8 * 4 * 32 * 1 * 129 * 4 + 255) // 256 * 256
+    assert n == (9 * 4 * 32 * 1 * 129 * 4 + 255) // 256 * 256
+    assert _native.lib().fa_decode_ticket_count(4, 32, 3) == 4 * 32 * 3
     assert _native.decode_workspace_bytes(0, 32, 1, 128, 8) == 0
 
 
