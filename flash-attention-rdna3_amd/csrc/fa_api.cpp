@@ -148,26 +148,54 @@ int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream) {
   return bwd_common(params, 1 << phase, stream);
 }
 
-int fa_decode_splitk(const fa_decode_params* params, void* stream) {
-  if (!params) return fail(FA_ERR_INVALID, "fa_decode_splitk: params is NULL");
+namespace {
+
+// Checks of fa_decode_splitk and fa_decode_splitk_noalloc (the latter brings
+// its own workspace and tickets, so it skips those two).
+int check_decode(const fa_decode_params* params, const char* who, bool own_scratch) {
+  if (!params) return fail(FA_ERR_INVALID, "%s: params is NULL", who);
   const fa_decode_params& p = *params;
-  if (p.abi_version != FA_ABI_VERSION) return fail(FA_ERR_INVALID, "fa_decode_splitk: abi_version mismatch");
+  if (p.abi_version != FA_ABI_VERSION) return fail(FA_ERR_INVALID, "%s: abi_version mismatch", who);
   if (p.dtype != FA_DTYPE_F16 && p.dtype != FA_DTYPE_BF16)
-    return fail(FA_ERR_INVALID, "fa_decode_splitk: dtype must be f16 or bf16");
-  if (!dim_ok(p.head_dim)) return fail(FA_ERR_UNSUPPORTED, "fa_decode_splitk: head_dim %d", p.head_dim);
+    return fail(FA_ERR_INVALID, "%s: dtype must be f16 or bf16", who);
+  if (!dim_ok(p.head_dim)) return fail(FA_ERR_UNSUPPORTED, "%s: head_dim %d", who, p.head_dim);
   if (p.batch <= 0 || p.heads_q <= 0 || p.heads_kv <= 0 || p.heads_q % p.heads_kv || p.seqlen_q <= 0 ||
       p.seqlen_k <= 0)
-    return fail(FA_ERR_INVALID, "fa_decode_splitk: bad shape");
-  if (p.num_splits < 1 || p.num_splits > 64) return fail(FA_ERR_INVALID, "fa_decode_splitk: num_splits");
-  if (p.kv_fp8 != 0 && p.kv_fp8 != 1) return fail(FA_ERR_INVALID, "fa_decode_splitk: kv_fp8 must be 0 or 1");
+    return fail(FA_ERR_INVALID, "%s: bad shape", who);
+  if (p.num_splits < 1 || p.num_splits > 64) return fail(FA_ERR_INVALID, "%s: num_splits", who);
+  if (p.kv_fp8 != 0 && p.kv_fp8 != 1) return fail(FA_ERR_INVALID, "%s: kv_fp8 must be 0 or 1", who);
   const int kes = p.kv_fp8 ? 1 : 2;
   if (!rows_ok(p.q, p.q_stride, 4, 2) || !rows_ok(p.k, p.k_stride, 4, kes) || !rows_ok(p.v, p.v_stride, 4, kes) ||
       !rows_ok(p.out, p.out_stride, 4, 2))
-    return fail(FA_ERR_INVALID, "fa_decode_splitk: q/k/v/out need a unit last stride and 16-byte aligned rows");
-  if (!p.workspace || !aligned16(p.workspace)) return fail(FA_ERR_INVALID, "fa_decode_splitk: workspace");
-  if ((reinterpret_cast<uintptr_t>(p.tickets) & 3u) != 0) return fail(FA_ERR_INVALID, "fa_decode_splitk: tickets");
-  if (p.causal != 0 && p.causal != 1) return fail(FA_ERR_INVALID, "fa_decode_splitk: causal must be 0 or 1");
-  return from_hip(fa::launch_decode(p, (hipStream_t)stream), "fa_decode_splitk");
+    return fail(FA_ERR_INVALID, "%s: q/k/v/out need a unit last stride and 16-byte aligned rows", who);
+  if (!own_scratch) {
+    if (!p.workspace || !aligned16(p.workspace)) return fail(FA_ERR_INVALID, "%s: workspace", who);
+    if ((reinterpret_cast<uintptr_t>(p.tickets) & 3u) != 0) return fail(FA_ERR_INVALID, "%s: tickets", who);
+  }
+  if (p.causal != 0 && p.causal != 1) return fail(FA_ERR_INVALID, "%s: causal must be 0 or 1", who);
+  return FA_OK;
+}
+
+}  // namespace
+
+int fa_decode_splitk(const fa_decode_params* params, void* stream) {
+  const int rc = check_decode(params, "fa_decode_splitk", false);
+  if (rc != FA_OK) return rc;
+  return from_hip(fa::launch_decode(*params, (hipStream_t)stream), "fa_decode_splitk");
+}
+
+int fa_decode_splitk_noalloc(const fa_decode_params* params, void* stream) {
+  const int rc = check_decode(params, "fa_decode_splitk_noalloc", true);
+  if (rc != FA_OK) return rc;
+  const fa_decode_params& p = *params;
+  const size_t ws = fa::decode_workspace_bytes(p.batch, p.heads_q, p.seqlen_q, p.head_dim, p.num_splits);
+  const size_t nt = (size_t)p.batch * p.heads_q * p.seqlen_q;
+  if (ws > FA_NOALLOC_WORKSPACE_BYTES || nt > FA_NOALLOC_TICKETS)
+    return fail(FA_ERR_INVALID,
+                "fa_decode_splitk_noalloc: needs %zu workspace bytes and %zu tickets; the static scratch holds "
+                "%d and %d (use fa_decode_splitk with a caller workspace)",
+                ws, nt, FA_NOALLOC_WORKSPACE_BYTES, FA_NOALLOC_TICKETS);
+  return from_hip(fa::launch_decode_noalloc(p, (hipStream_t)stream), "fa_decode_splitk_noalloc");
 }
 
 int fa_decode_paged(const fa_paged_params* params, void* stream) {

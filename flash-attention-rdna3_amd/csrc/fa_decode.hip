@@ -22,6 +22,8 @@
 //  * the 4 wave states (max, sum, O^T) are merged in LDS at the end, so one
 //    partial per workgroup reaches HBM.  With a single split the merged row
 //    is written straight to `out` and no combine kernel runs.
+#include <mutex>
+
 #include "fa_internal.hpp"
 #include "fa_tiles.hpp"
 
@@ -428,6 +430,48 @@ hipError_t launch_decode(const fa_decode_params& p, hipStream_t s) {
   split_workspace(a, p.workspace);
   a.tickets = p.tickets;
   return decode_dispatch<false>(p.dtype, a, s);
+}
+
+// ---------------------------------------------------------------------------
+// Static scratch of fa_decode_splitk_noalloc: the arrival counters first
+// (zero at load, left zero by every call), then the split workspace.  Host
+// code never passes `scratch` itself to a kernel (in host code the name is a
+// stand-in, not a device address): each device's address is looked up once
+// with hipGetSymbolAddress, with that device current, and kept per device.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoallocTicketBytes = (size_t)FA_NOALLOC_TICKETS * 4;
+static __device__ __align__(256) unsigned char scratch[kNoallocTicketBytes + FA_NOALLOC_WORKSPACE_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_ptr[kMaxDevices] = {};
+
+hipError_t scratch_for_current_device(unsigned char** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = static_cast<unsigned char*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+}  // namespace
+
+hipError_t launch_decode_noalloc(const fa_decode_params& p, hipStream_t s) {
+  unsigned char* base = nullptr;
+  hipError_t e = scratch_for_current_device(&base);
+  if (e != hipSuccess) return e;
+  fa_decode_params q = p;
+  q.tickets = reinterpret_cast<uint32_t*>(base);
+  q.workspace = base + kNoallocTicketBytes;
+  return launch_decode(q, s);
 }
 
 hipError_t launch_paged(const fa_paged_params& p, hipStream_t s) {

@@ -21,6 +21,9 @@ hipError_t launch_fwd(const fa_fwd_params& p, hipStream_t stream);
 // phases: bit 0 delta, bit 1 dK/dV, bit 2 dQ.
 hipError_t launch_bwd(const fa_bwd_params& p, int phases, hipStream_t stream);
 hipError_t launch_decode(const fa_decode_params& p, hipStream_t stream);
+// launch_decode with the library's static per-device scratch as workspace and
+// tickets (sizes already checked against FA_NOALLOC_*).
+hipError_t launch_decode_noalloc(const fa_decode_params& p, hipStream_t stream);
 hipError_t launch_paged(const fa_paged_params& p, hipStream_t stream);
 hipError_t launch_tiny(const fa_tiny_params& p, hipStream_t stream);
 hipError_t launch_append(const fa_append_params& p, hipStream_t stream);

@@ -120,7 +120,8 @@ _STRUCTS = (FwdParams, BwdParams, DecodeParams, PagedParams, TinyParams, AppendP
 EXPORTS = (
     "fa_abi_version", "fa_last_error_string", "fa_params_size", "fa_decode_workspace_bytes",
     "fa_decode_ticket_count",
-    "fa_fwd", "fa_bwd", "fa_bwd_phase", "fa_decode_splitk", "fa_decode_paged", "fa_tiny_fwd_f32",
+    "fa_fwd", "fa_bwd", "fa_bwd_phase", "fa_decode_splitk", "fa_decode_splitk_noalloc", "fa_decode_paged",
+    "fa_tiny_fwd_f32",
     "fa_kvcache_append",
 )
 
@@ -155,7 +156,8 @@ def lib():
         handle.fa_decode_ticket_count.restype = ctypes.c_size_t
         handle.fa_decode_ticket_count.argtypes = [ctypes.c_int] * 3
         for name, struct in (("fa_fwd", FwdParams), ("fa_bwd", BwdParams),
-                             ("fa_decode_splitk", DecodeParams), ("fa_decode_paged", PagedParams),
+                             ("fa_decode_splitk", DecodeParams), ("fa_decode_splitk_noalloc", DecodeParams),
+                             ("fa_decode_paged", PagedParams),
                              ("fa_tiny_fwd_f32", TinyParams), ("fa_kvcache_append", AppendParams)):
             fn = getattr(handle, name)
             fn.restype = ctypes.c_int

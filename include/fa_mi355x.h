@@ -312,6 +312,26 @@ int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream);
 size_t fa_decode_ticket_count(int batch, int heads_q, int seqlen_q);
 
 int fa_decode_splitk(const fa_decode_params* params, void* stream);
+
+/*
+ * fa_decode_splitk without any caller scratch and without any allocation.
+ *
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, and
+ * harnesses that forbid hipMalloc.  `workspace` and `tickets` in params are
+ * ignored.  The split partials and the merge's arrival counters live in a
+ * static scratch array of FA_NOALLOC_WORKSPACE_BYTES + 4 * FA_NOALLOC_TICKETS
+ * bytes, one per GPU, held until the process ends.  A call that would need
+ * more (fa_decode_workspace_bytes(...) > FA_NOALLOC_WORKSPACE_BYTES, or
+ * batch * heads_q * seqlen_q > FA_NOALLOC_TICKETS) fails with FA_ERR_INVALID.
+ * Every call on one GPU shares that GPU's scratch: calls that overlap in time
+ * on one GPU (different streams, or host threads) race and must be
+ * serialised by the caller.  The counters start at zero when the library
+ * loads and every call leaves them at zero.
+ */
+#define FA_NOALLOC_WORKSPACE_BYTES (32 * 1024 * 1024)
+#define FA_NOALLOC_TICKETS 65536
+int fa_decode_splitk_noalloc(const fa_decode_params* params, void* stream);
 int fa_decode_paged(const fa_paged_params* params, void* stream);
 int fa_tiny_fwd_f32(const fa_tiny_params* params, void* stream);
 int fa_kvcache_append(const fa_append_params* params, void* stream);
