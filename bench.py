@@ -437,6 +437,52 @@ def cpu_baseline(budget_s=20.0):
             "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": threads}
 
 
+def pmc_summary(dirs):
+    """Markdown table of rocprofv3 --pmc results (one directory per counter
+    pass, each holding run_results.db): per kernel and grid, the average per
+    dispatch of every counter, plus the derived MFMA figures."""
+    import glob
+    import sqlite3
+    from collections import defaultdict
+
+    acc = defaultdict(lambda: defaultdict(list))
+    dur = defaultdict(list)
+    for d in dirs:
+        for db in glob.glob(os.path.join(d, "**", "*results.db"), recursive=True):
+            con = sqlite3.connect(db)
+            q = "select dispatch_id, kernel_name, grid_size, counter_name, value, duration from counters_collection"
+            for disp, name, grid, cname, value, duration in con.execute(q):
+                if "fa::" not in name:
+                    continue
+                key = (name.split("(")[0].replace("void fa::", ""), int(grid))
+                acc[key][cname].append(float(value))
+                dur[key].append(float(duration))
+    simds = 256 * 4
+    rows = []
+    for key in sorted(acc, key=lambda k: -sum(dur[k]) / len(dur[k])):
+        c = {n: sum(v) / len(v) for n, v in acc[key].items()}
+        us = sum(dur[key]) / len(dur[key]) / 1e3
+        mops = c.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0) + c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
+        tf = mops * 512 / (us * 1e-6) / 1e12 if us else 0.0
+        # GRBM_GUI_ACTIVE counts GPU-busy cycles of the dispatch (summed over
+        # the 8 XCDs): cycles per XCD = value / 8.
+        cyc = c.get("GRBM_GUI_ACTIVE", 0.0) / 8
+        busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (cyc * simds) if cyc else 0.0
+        mf = c.get("SQ_INSTS_MFMA", 0.0)
+        rows.append((key, us, cyc / us / 1e3 if us else 0.0, tf, busy, c.get("SQ_INSTS_LDS", 0.0) / mf if mf else 0.0,
+                     c.get("SQ_INSTS_VALU", 0.0) / mf if mf else 0.0, c))
+    print("| kernel | grid | avg us | clock GHz | MFMA TFLOP/s (MOPS x 512) | MFMA busy | LDS / MFMA inst | VALU / MFMA inst |")
+    print("|---|---|---|---|---|---|---|---|")
+    for (name, grid), us, ghz, tf, busy, lpm, vpm, _ in rows:
+        print(f"| `{name}` | {grid} | {us:.1f} | {ghz:.2f} | {tf:.0f} | {busy * 100:.1f} % | {lpm:.2f} | {vpm:.2f} |")
+    print()
+    names = sorted({n for *_, c in rows for n in c})
+    print("| kernel | grid | " + " | ".join(names) + " |")
+    print("|---|---|" + "---|" * len(names))
+    for (name, grid), *_, c in rows:
+        print(f"| `{name}` | {grid} | " + " | ".join(f"{c[n]:.4g}" if n in c else "" for n in names) + " |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -446,7 +492,12 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="skip decode/varlen side measurements")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 10 device copies of MIB MiB (scales rocprofv3 FETCH/WRITE_SIZE)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="only summarise rocprofv3 --pmc result directories as markdown")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
     if args.copy_calibration:
         n = args.copy_calibration * 1024 * 1024
         src = torch.ones(n, dtype=torch.uint8, device="cuda")
