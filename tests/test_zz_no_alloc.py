@@ -84,3 +84,32 @@ def test_noalloc_rejects_oversized_calls():
     p = _params(q, k, k, torch.empty_like(q), lens, 64)
     rc, msg = _call("fa_decode_splitk_noalloc", p)
     assert rc != 0 and "static scratch" in msg
+
+
+def test_noalloc_replays_under_hip_graph_capture():
+    # The entry point's purpose: a call recorded in a HIP graph (no
+    # allocation, no memset node) replays correctly, with eager work and
+    # synchronisations between the replays, against the eager result.
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(2, 32, 1, 128, generator=g).half().to(DEVICE)
+    k = torch.randn(2, 8, 4096, 128, generator=g).half().to(DEVICE)
+    v = torch.randn(2, 8, 4096, 128, generator=g).half().to(DEVICE)
+    lens = torch.tensor([4000, 1500], dtype=torch.int32, device=DEVICE)
+    splits = 8
+    eager = torch.empty_like(q)
+    assert _call("fa_decode_splitk_noalloc", _params(q, k, v, eager, lens, splits))[0] == 0
+    torch.cuda.synchronize()
+    out = torch.zeros_like(q)
+    p = _params(q, k, v, out, lens, splits)
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        rc, msg = _call("fa_decode_splitk_noalloc", p)
+    assert rc == 0, msg
+    for i in range(4):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, eager, atol=0, rtol=0)
+        _ = (k[:, :, :64].float() * (i + 1)).sum().item()  # eager work between replays
