@@ -275,7 +275,11 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
         };
         using T_ = std::true_type;
         using F_ = std::false_type;
-        if constexpr (MODE >= 1) {
+        if constexpr (MODE == 3) {
+          // softcap only
+          if (vis == 1) scores(F_{}, T_{}, std::integral_constant<int, 0>{}, F_{}, T_{});
+          else scores(F_{}, T_{}, std::integral_constant<int, 0>{}, F_{}, F_{});
+        } else if constexpr (MODE >= 1) {
           if (vis == 1) dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_, T_{}); });
           else dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_, F_{}); });
         } else {
@@ -567,7 +571,11 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
       };
       using T_ = std::true_type;
       using F_ = std::false_type;
-      if constexpr (MODE >= 1) {
+      if constexpr (MODE == 3) {
+        // softcap only
+        if (vis == 1) scores(F_{}, T_{}, std::integral_constant<int, 0>{}, F_{}, T_{});
+        else scores(F_{}, T_{}, std::integral_constant<int, 0>{}, F_{}, F_{});
+      } else if constexpr (MODE >= 1) {
         if (vis == 1) dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_, T_{}); });
         else dispatch_mods(md, [&](auto a, auto b_, auto c_) { scores(F_{}, a, b_, c_, F_{}); });
       } else {

@@ -598,9 +598,10 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
     return hipSuccess;
   }
   }
+  constexpr int GMODE = MODE == 3 ? 1 : MODE;  // no softcap-only generic variant
   if (phases & 2) {
     using C = DkdvCfg<Tag, D>;
-    auto kern = bwd_dkdv_kernel<Tag, D, MODE>;
+    auto kern = bwd_dkdv_kernel<Tag, D, GMODE>;
     hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
     if (e != hipSuccess) return e;
     const int nnb = (f.seqlen_k + C::BN - 1) / C::BN;
@@ -611,7 +612,7 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
   }
   if (phases & 4) {
     using C = DqCfg<Tag, D>;
-    auto kern = bwd_dq_kernel<Tag, D, MODE>;
+    auto kern = bwd_dq_kernel<Tag, D, GMODE>;
     hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
     if (e != hipSuccess) return e;
     const int nmb = (f.seqlen_q + C::BM - 1) / C::BM;
@@ -639,6 +640,8 @@ template <typename Tag>
 hipError_t bwd_by_mods(const fa_bwd_params& p, int ph, hipStream_t s) {
   const fa_fwd_params& f = p.fwd;
   if (f.dropout_p > 0.f) return bwd_by_dim<Tag, 2>(p, ph, s);
+  if constexpr (!std::is_same<Tag, f32_t>::value)
+    if (f.softcap > 0.f && !f.bias && !f.alibi_slopes) return bwd_by_dim<Tag, 3>(p, ph, s);
   if (f.softcap > 0.f || f.bias || f.alibi_slopes) return bwd_by_dim<Tag, 1>(p, ph, s);
   return bwd_by_dim<Tag, 0>(p, ph, s);
 }

@@ -207,7 +207,11 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
         };
         using T_ = std::true_type;
         using F_ = std::false_type;
-        if constexpr (MODE == 1) {
+        if constexpr (MODE == 3) {
+          // softcap only: one variant per visibility instead of all modifier sets
+          if (vis == 1) masked_scores(T_{}, std::integral_constant<int, 0>{}, F_{}, T_{});
+          else masked_scores(T_{}, std::integral_constant<int, 0>{}, F_{}, F_{});
+        } else if constexpr (MODE == 1) {
           if (vis == 1) dispatch_mods(md, [&](auto a, auto b_, auto c_) { masked_scores(a, b_, c_, T_{}); });
           else dispatch_mods(md, [&](auto a, auto b_, auto c_) { masked_scores(a, b_, c_, F_{}); });
         } else if constexpr (MODE == 2) {

@@ -288,8 +288,10 @@ static hipError_t run_fwd(const fa_fwd_params& p, hipStream_t stream) {
     return hipGetLastError();
     }
   }
+  // The generic kernel has no softcap-only variant (MODE 3 is MODE 1 there).
+  constexpr int GMODE = MODE == 3 ? 1 : MODE;
   using C = FwdCfg<Tag, D>;
-  auto kern = fwd_kernel<Tag, D, MODE>;
+  auto kern = fwd_kernel<Tag, D, GMODE>;
   hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
   if (e != hipSuccess) return e;
   const int nmb = (p.seqlen_q + C::BM - 1) / C::BM;
@@ -313,8 +315,11 @@ static hipError_t fwd_by_dim(const fa_fwd_params& p, hipStream_t s) {
 
 template <typename Tag>
 hipError_t fwd_by_mods(const fa_fwd_params& p, hipStream_t s) {
-  // 0: plain, 1: softcap / bias / ALiBi, 2: also dropout (Philox per score).
+  // 0: plain, 1: softcap / bias / ALiBi, 2: also dropout (Philox per score),
+  // 3: softcap without bias or ALiBi (16-bit kernels; one score variant).
   if (p.dropout_p > 0.f) return fwd_by_dim<Tag, 2>(p, s);
+  if constexpr (!std::is_same<Tag, f32_t>::value)
+    if (p.softcap > 0.f && !p.bias && !p.alibi_slopes) return fwd_by_dim<Tag, 3>(p, s);
   if (p.softcap > 0.f || p.bias || p.alibi_slopes) return fwd_by_dim<Tag, 1>(p, s);
   return fwd_by_dim<Tag, 0>(p, s);
 }
