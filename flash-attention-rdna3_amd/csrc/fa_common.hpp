@@ -207,7 +207,8 @@ __device__ inline float philox_uniform(uint64_t seed, uint64_t offset) {
 struct Mods {
   float scale_log2;   // softmax_scale * log2(e)
   float cap2;         // softcap * log2(e), 0 = off
-  float inv_cap2;     // 1 / cap2 (0 when off)
+  float cap_k;        // 2 log2(e) * softmax_scale / softcap: exp2 argument of e^{2y}
+  float cap2_m2;      // -2 * cap2
   const void* bias;   // already offset to (batch, head); NULL = off
   int bias_f32;       // bias element type: 1 fp32, 0 q dtype
   int bias_bf16;      // q dtype is bf16 (only meaningful when !bias_f32)
@@ -224,12 +225,16 @@ struct Mods {
   int64_t drop_sk;    // Sk of the dense problem
 };
 
-__device__ inline float tanh_fast(float y) {
-  // tanh(y) = sign(y) * (1 - e^{-2|y|}) / (1 + e^{-2|y|}), e^{-2|y|} <= 1:
-  // hardware exp2 and reciprocal (about 1 ulp each), no division sequence.
-  const float t = __builtin_amdgcn_exp2f(fabsf(y) * (-2.0f * kLog2e));
-  const float r = (1.f - t) * __builtin_amdgcn_rcpf(1.f + t);
-  return copysignf(r, y);
+// Softcapped log2-domain score x = cap2 * tanh(s * scale / cap) of the raw dot
+// product s, and tcap = tanh(s * scale / cap) (for the backward), from
+// tanh(y) = 1 - 2 / (1 + e^{2y}): one hardware exp2 and one reciprocal.
+// Saturates to +-1 without a sign split (e^{2y} -> inf gives 1, -> 0 gives
+// -1); the absolute error of tcap is a few 2^-24, which is what the
+// exp2 of the softmax sees (x's error is cap2 times that).
+__device__ inline float softcap_score(const Mods& md, float s, float& tcap) {
+  const float r = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s * md.cap_k));
+  tcap = __builtin_fmaf(-2.f, r, 1.f);
+  return __builtin_fmaf(md.cap2_m2, r, md.cap2);
 }
 
 // Visible keys of row m form [lo, hi] (empty when hi < lo).  The mode flags
@@ -261,8 +266,7 @@ __device__ inline float score(const Mods& md, float s, int m, int n, float& tcap
   tcap = 0.f;
   if constexpr (MODS) {
     if (md.cap2 > 0.f) {
-      tcap = tanh_fast(x * md.inv_cap2);
-      x = md.cap2 * tcap;
+      x = softcap_score(md, s, tcap);
     }
     if (md.bias) x += load_bias(md, m, n) * kLog2e;
     if (md.has_alibi) x -= md.alibi_log2 * fabsf((float)(n - m - md.off));
@@ -287,8 +291,7 @@ __device__ inline float score_m(const Mods& md, float s, int m, int n, float& tc
   float x = s * md.scale_log2;
   tcap = 0.f;
   if constexpr (CAP) {
-    tcap = tanh_fast(x * md.inv_cap2);
-    x = md.cap2 * tcap;
+    x = softcap_score(md, s, tcap);
   }
   if constexpr (BIASK != 0) x += load_bias_k<BIASK>(md, m, n) * kLog2e;
   if constexpr (ALIBI) x -= md.alibi_log2 * fabsf((float)(n - m - md.off));
@@ -409,7 +412,8 @@ __device__ inline Mods make_mods(const fa_fwd_params& p, int b, int hq, int sq, 
   Mods md;
   md.scale_log2 = p.softmax_scale * kLog2e;
   md.cap2 = p.softcap * kLog2e;
-  md.inv_cap2 = md.cap2 > 0.f ? 1.f / md.cap2 : 0.f;
+  md.cap_k = p.softcap > 0.f ? 2.f * kLog2e * p.softmax_scale / p.softcap : 0.f;
+  md.cap2_m2 = -2.f * md.cap2;
   md.bias = nullptr;
   md.bias_f32 = p.bias_dtype == FA_DTYPE_F32;
   md.bias_bf16 = p.dtype == FA_DTYPE_BF16;
