@@ -185,12 +185,17 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
         // MODE 0 seeds the score accumulators with -lse2/c and -delta (the
         // MFMAs then produce s - lse2/c and dP - delta directly); the other
         // modes need the raw scores and keep lse2 / delta.
-        lf[htid] = (MODE == 0) ? -l2v / md.scale_log2 : l2v;
+        // MODE 3 keeps cap2 - lse2: exp2(x - lse2) is then one FMA on the
+        // softcap's r away (x = cap2 - 2 cap2 r).
+        lf[htid] = (MODE == 0) ? -l2v / md.scale_log2 : (MODE == 3) ? md.cap2 - l2v : l2v;
         lf[C::BMQ + htid] = (MODE != 2) ? -dreg : dreg;
       }
     };
 
     const VisBounds kvb = key_block_bounds(md, n0w, ncols);
+    // Visible rows of this lane's key, relative to the row of slot 0.
+    int rlo, rhi;
+    row_bounds(md, n, rlo, rhi);
     if (my_count > 0) {
       const int m_first = mlo + my_first * C::BMQ;
       load_stage(m_first, 0);
@@ -239,17 +244,25 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
         // body: a per-element choice would become one branch per score.
         // MASK: the block is partly visible (vis == 1); fully visible blocks
         // skip the per-score visibility test.
+        const Span rs = make_span(rlo, rhi, m0 + 4 * h);
         auto scores = [&](auto plain_t, auto cap_t, auto bias_t, auto alibi_t, auto mask_t) {
           (void)plain_t;  // the dK/dV body has no separate plain path
           constexpr bool CAP = decltype(cap_t)::value;
           constexpr bool MASK = decltype(mask_t)::value;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            float pv, tc = 0.f;
+            float pv, tc = 0.f, capq = 0.f;
             if constexpr (MODE == 0) {
               // sacc = s - lse2/c, pacc = dP - delta (seeded accumulators).
               pv = __builtin_amdgcn_exp2f(sacc[i] * c);
-              if constexpr (MASK) pv = !keep_pos(md, m0 + acc_row(i, h), n) ? 0.f : pv;
+              if constexpr (MASK) pv = in_span(rs, acc_row(i, 0)) ? pv : 0.f;
+            } else if constexpr (MODE == 3) {
+              // L2 holds cap2 - lse2; capq = (1 - tanh^2) / 4 (the 4 is
+              // applied to dK at the end).
+              const float r = softcap_r(md, sacc[i]);
+              pv = __builtin_amdgcn_exp2f(__builtin_fmaf(md.cap2_m2, r, L2[8 * (i / 4) + 4 * h + (i % 4)]));
+              capq = __builtin_fmaf(-r, r, r);
+              if constexpr (MASK) pv = in_span(rs, acc_row(i, 0)) ? pv : 0.f;
             } else {
               const int m = m0 + acc_row(i, h);
               const float x = score_m<CAP, decltype(bias_t)::value, decltype(alibi_t)::value>(md, sacc[i], m, n, tc);
@@ -257,7 +270,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
               // the stage (register pressure of the modifier variants).
               const float l2i = L2[8 * (i / 4) + 4 * h + (i % 4)];
               pv = __builtin_amdgcn_exp2f(x - l2i);
-              if constexpr (MASK) pv = !keep_pos(md, m, n) ? 0.f : pv;
+              if constexpr (MASK) pv = in_span(rs, acc_row(i, 0)) ? pv : 0.f;
             }
             float dp = pacc[i], pd = pv;
             if constexpr (MODE == 2) {
@@ -268,7 +281,8 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
               }
             }
             float ds = (MODE != 2) ? pv * dp : pv * (dp - dl[i]);
-            if constexpr (CAP) ds *= (1.f - tc * tc);
+            if constexpr (MODE == 3) ds *= capq;
+            else if constexpr (CAP) ds *= (1.f - tc * tc);
             sacc[i] = pd;
             pacc[i] = ds;
           }
@@ -332,7 +346,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
            (int64_t)(k_start + n) * p.dk_stride[2];
   S* dvr = reinterpret_cast<S*>(p.dv) + b * p.dv_stride[0] + hk * p.dv_stride[1] +
            (int64_t)(k_start + n) * p.dv_stride[2];
-  const float sc = f.softmax_scale;
+  const float sc = f.softmax_scale * (MODE == 3 ? 4.f : 1.f);
 #pragma unroll
   for (int db = 0; db < C::NDB; ++db)
 #pragma unroll
@@ -520,6 +534,17 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
     }
   }
 
+  // Visible keys of this lane's row, and the constants of the score loop:
+  // cap2 - lse2 (MODE 3: exp2(x - lse2) is one FMA on the softcap's r) and
+  // the dP accumulator seed (-delta in MODES 1 and 3, so the MFMAs produce
+  // dP - delta).
+  int klo, khi;
+  key_bounds(md, m, klo, khi);
+  const float capl = md.cap2 - lse2;
+  f32x16 dseed;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) dseed[i] = (MODE == 1 || MODE == 3) ? -dlt : 0.f;
+
   wait_vm_all();
   __syncthreads();
   for (int t = 0; t < nh0; ++t) {
@@ -532,7 +557,7 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
       const S* Vs = Ks + C::KT;
       f32x16 sacc[C::NKB], pacc[C::NKB];
 #pragma unroll
-      for (int kb2 = 0; kb2 < C::NKB; ++kb2) { sacc[kb2] = zero16(); pacc[kb2] = zero16(); }
+      for (int kb2 = 0; kb2 < C::NKB; ++kb2) { sacc[kb2] = zero16(); pacc[kb2] = dseed; }
 #pragma unroll
       for (int s = 0; s < C::NSTEP; ++s)
 #pragma unroll
@@ -543,6 +568,7 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
       if constexpr (MODE == 0) sched_read_ahead<2 * C::NSTEP * C::NKB, 4>();
       // MASK: the tile is partly visible (vis == 1); fully visible tiles
       // skip the per-score visibility test.
+      const Span ks = make_span(klo, khi, n0 + 4 * h);
       auto scores = [&](auto plain_t, auto cap_t, auto bias_t, auto alibi_t, auto mask_t) {
         constexpr bool plain = decltype(plain_t)::value;
         constexpr bool CAP = decltype(cap_t)::value;
@@ -551,21 +577,35 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
         for (int kb2 = 0; kb2 < C::NKB; ++kb2)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            float pv, tc = 0.f;
+            float pv, tc = 0.f, capq = 0.f;
             const int nn = n0 + kb2 * 32 + acc_row(i, h);
             if constexpr (plain) {
               pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb2][i], c, -lse2));
+            } else if constexpr (MODE == 3) {
+              // capq = (1 - tanh^2) / 4 (the 4 is applied to dQ at the end)
+              const float r = softcap_r(md, sacc[kb2][i]);
+              pv = __builtin_amdgcn_exp2f(__builtin_fmaf(md.cap2_m2, r, capl));
+              capq = __builtin_fmaf(-r, r, r);
+              if constexpr (MASK) pv = in_span(ks, kb2 * 32 + acc_row(i, 0)) ? pv : 0.f;
             } else {
               const float x = score_m<CAP, decltype(bias_t)::value, decltype(alibi_t)::value>(md, sacc[kb2][i], m, nn, tc);
               pv = __builtin_amdgcn_exp2f(x - lse2);
-              if constexpr (MASK) pv = !keep_pos(md, m, nn) ? 0.f : pv;
+              if constexpr (MASK) pv = in_span(ks, kb2 * 32 + acc_row(i, 0)) ? pv : 0.f;
             }
             float dp = pacc[kb2][i];
-            if constexpr (MODE == 2) {
-              if (md.drop_p > 0.f) dp = dropout_keep(md, m, nn) ? dp * md.drop_scale : 0.f;
+            float ds;
+            if constexpr (MODE == 1 || MODE == 3) {
+              ds = pv * dp;  // dp - delta: the accumulator was seeded with -delta
+            } else {
+              // (MODE 0 keeps a zero seed: the seed's registers, live across
+              // the loop, cost it more than the subtraction, measured)
+              if constexpr (MODE == 2) {
+                if (md.drop_p > 0.f) dp = dropout_keep(md, m, nn) ? dp * md.drop_scale : 0.f;
+              }
+              ds = pv * (dp - dlt);
             }
-            float ds = pv * (dp - dlt);
-            if constexpr (CAP) ds *= (1.f - tc * tc);
+            if constexpr (MODE == 3) ds *= capq;
+            else if constexpr (CAP) ds *= (1.f - tc * tc);
             sacc[kb2][i] = ds;
           }
       };
@@ -612,7 +652,7 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
   if (!mvalid) return;
   S* dqr = reinterpret_cast<S*>(p.dq) + b * p.dq_stride[0] + hq * p.dq_stride[1] +
            (int64_t)(q_start + m) * p.dq_stride[2];
-  const float sc = f.softmax_scale;
+  const float sc = f.softmax_scale * (MODE == 3 ? 4.f : 1.f);
 #pragma unroll
   for (int db = 0; db < C::NDB; ++db)
 #pragma unroll

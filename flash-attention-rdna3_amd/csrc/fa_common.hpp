@@ -231,11 +231,30 @@ struct Mods {
 // Saturates to +-1 without a sign split (e^{2y} -> inf gives 1, -> 0 gives
 // -1); the absolute error of tcap is a few 2^-24, which is what the
 // exp2 of the softmax sees (x's error is cap2 times that).
+// In terms of r = 1 / (1 + e^{2y}): x = cap2 - 2 cap2 r, tcap = 1 - 2r and
+// (1 - tcap^2) / 4 = r - r^2.  x falls as r grows; a hidden score (x = -inf)
+// is r = +inf.
+__device__ inline float softcap_r(const Mods& md, float s) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s * md.cap_k));
+}
 __device__ inline float softcap_score(const Mods& md, float s, float& tcap) {
-  const float r = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s * md.cap_k));
+  const float r = softcap_r(md, s);
   tcap = __builtin_fmaf(-2.f, r, 1.f);
   return __builtin_fmaf(md.cap2_m2, r, md.cap2);
 }
+
+// A visibility interval [lo, hi] of positions base + k, held relative to
+// base so the per-score test compares the compile-time offset k against two
+// registers (no per-score address arithmetic).  Bounds are clamped to
+// +-2^30 first, so the subtraction cannot overflow.
+struct Span {
+  int lo, hi;
+};
+__device__ inline Span make_span(int lo, int hi, int base) {
+  constexpr int kBig = 1 << 30;
+  return Span{max(lo, -kBig) - base, min(hi, kBig) - base};
+}
+__device__ inline bool in_span(const Span& s, int k) { return (k >= s.lo) & (k <= s.hi); }
 
 // Visible keys of row m form [lo, hi] (empty when hi < lo).  The mode flags
 // are wave-uniform, so the bounds are scalar selects.
@@ -243,6 +262,15 @@ __device__ inline void key_bounds(const Mods& md, int m, int& lo, int& hi) {
   const int qp = m + md.off;
   hi = min(md.seqlen_k - 1, min(md.causal ? qp : INT_MAX, md.wr >= 0 ? qp + md.wr : INT_MAX));
   lo = md.wl >= 0 ? qp - md.wl : INT_MIN;
+}
+
+// Visible query rows of key n form [lo, hi] (empty when hi < lo): the
+// transpose of key_bounds.
+__device__ inline void row_bounds(const Mods& md, int n, int& lo, int& hi) {
+  constexpr int kBig = 1 << 30;
+  lo = max(md.causal ? n : -kBig, md.wr >= 0 ? n - md.wr : -kBig) - md.off;
+  hi = (md.wl >= 0 ? n + md.wl : kBig) - md.off;
+  if (n >= md.seqlen_k) { lo = kBig; hi = -kBig; }
 }
 
 __device__ inline bool keep_pos(const Mods& md, int m, int n) {

@@ -189,6 +189,7 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
         // This lane's visible keys (its row is fixed): one interval per tile.
         int klo = INT_MIN, khi = INT_MAX;
         if (vis == 1) key_bounds(md, m, klo, khi);
+        const Span ks = make_span(klo, khi, n0 + 4 * h);
         // MASK: the tile is partly visible (vis == 1); a fully visible tile
         // with modifiers skips the per-score interval test.
         auto masked_scores = [&](auto cap_t, auto bias_t, auto alibi_t, auto mask_t) {
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
               float tc;
               float x = score_m<decltype(cap_t)::value, decltype(bias_t)::value, decltype(alibi_t)::value>(
                   md, sacc[kb2][i], m, n, tc);
-              if constexpr (decltype(mask_t)::value) x = ((n >= klo) & (n <= khi)) ? x : kNegInf;
+              if constexpr (decltype(mask_t)::value) x = in_span(ks, kb2 * 32 + acc_row(i, 0)) ? x : kNegInf;
               sacc[kb2][i] = x;
               tmax = fmaxf(tmax, x);
             }
@@ -208,9 +209,24 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
         using T_ = std::true_type;
         using F_ = std::false_type;
         if constexpr (MODE == 3) {
-          // softcap only: one variant per visibility instead of all modifier sets
-          if (vis == 1) masked_scores(T_{}, std::integral_constant<int, 0>{}, F_{}, T_{});
-          else masked_scores(T_{}, std::integral_constant<int, 0>{}, F_{}, F_{});
+          // Softcap only.  The tile keeps the softcap's r (x = cap2 - 2 cap2 r
+          // falls as r grows, a hidden score is r = +inf): the row max comes
+          // from the least r and exp2(x - m) is one FMA on r.
+          float rmin = __builtin_inff();
+          auto rscores = [&](auto mask_t) {
+#pragma unroll
+            for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) {
+                float r = softcap_r(md, sacc[kb2][i]);
+                if constexpr (decltype(mask_t)::value) r = in_span(ks, kb2 * 32 + acc_row(i, 0)) ? r : __builtin_inff();
+                sacc[kb2][i] = r;
+                rmin = fminf(rmin, r);
+              }
+          };
+          if (vis == 1) rscores(T_{});
+          else rscores(F_{});
+          tmax = __builtin_fmaf(md.cap2_m2, rmin, md.cap2);
         } else if constexpr (MODE == 1) {
           if (vis == 1) dispatch_mods(md, [&](auto a, auto b_, auto c_) { masked_scores(a, b_, c_, T_{}); });
           else dispatch_mods(md, [&](auto a, auto b_, auto c_) { masked_scores(a, b_, c_, F_{}); });
@@ -240,6 +256,16 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb2][i], c, mc));
+            sacc[kb2][i] = pv;
+            rsum += pv;
+          }
+      } else if constexpr (MODE == 3) {
+        const float cm = md.cap2 - m_use;
+#pragma unroll
+        for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(md.cap2_m2, sacc[kb2][i], cm));
             sacc[kb2][i] = pv;
             rsum += pv;
           }
