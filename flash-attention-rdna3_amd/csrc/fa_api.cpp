@@ -143,6 +143,11 @@ static int bwd_common(const fa_bwd_params* params, int phases, void* stream) {
 
 int fa_bwd(const fa_bwd_params* params, void* stream) { return bwd_common(params, 7, stream); }
 
+size_t fa_bwd_workspace_bytes(const fa_bwd_params* params) {
+  if (!params) return 0;
+  return fa::bwd_ds_bytes(*params);
+}
+
 int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream) {
   if (phase < 0 || phase > 2) return fail(FA_ERR_INVALID, "fa_bwd_phase: phase %d not in 0..2", phase);
   return bwd_common(params, 1 << phase, stream);

@@ -7,6 +7,21 @@ namespace fa {
 template <typename Tag>
 hipError_t bwd_by_mods(const fa_bwd_params& p, int ph, hipStream_t s);
 
+size_t bwd_ds_bytes(const fa_bwd_params& p) {
+  const fa_fwd_params& f = p.fwd;
+  if (f.dtype == FA_DTYPE_F32 || f.head_dim > 128) return 0;
+  if (f.batch <= 0 || f.heads_q <= 0 || f.seqlen_q <= 0 || f.seqlen_k <= 0) return 0;
+  int64_t elems;
+  if (f.cu_seqlens_q) {
+    if (f.batch > kDsMaxVarlenBatch || f.total_q < 0) return 0;
+    // sum_b Sk_b * pitch(Sq_b) <= max_seqlen_k * (total_q + 31 * batch)
+    elems = (int64_t)f.heads_q * f.seqlen_k * ((int64_t)f.total_q + 31 * (int64_t)f.batch);
+  } else {
+    elems = (int64_t)f.batch * f.heads_q * f.seqlen_k * ds_pitch(f.seqlen_q);
+  }
+  return (size_t)elems * 2 + 1024;
+}
+
 hipError_t launch_bwd(const fa_bwd_params& p, int ph, hipStream_t s) {
   switch (p.fwd.dtype) {
     case FA_DTYPE_F16: return bwd_by_mods<f16_t>(p, ph, s);

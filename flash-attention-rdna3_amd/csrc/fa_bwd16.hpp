@@ -18,9 +18,37 @@
 #include "fa_internal.hpp"
 #include "fa_tiles.hpp"
 
+#ifndef FA_DS_DUMP
+#define FA_DS_DUMP 0
+#endif
+
 namespace fa {
 
 __device__ inline float lse2_of(float lse) { return lse == kNegInf ? __builtin_inff() : lse * kLog2e; }
+
+// Start (elements) of the dS region of (sequence b, query head hq) in the
+// scratch, or -1 when it would not fit (varlen lengths inconsistent with
+// max_seqlen / total): then nothing is stored there or read from it.
+__device__ inline int64_t ds_region(const fa_bwd_params& p, int b, int hq, int sq, int sk) {
+  const fa_fwd_params& f = p.fwd;
+  int64_t base;
+  if (!f.cu_seqlens_q) {
+    base = (int64_t)b * f.heads_q * sk * ds_pitch(sq);
+  } else {
+    int64_t acc = 0;
+    for (int i = 0; i < b; ++i) {
+      int s0, l0, s1, l1;
+      bounded_seq(f.cu_seqlens_q, i, f.total_q, s0, l0);
+      bounded_seq(f.cu_seqlens_k, i, f.total_k, s1, l1);
+      acc += (int64_t)l1 * ds_pitch(l0);
+    }
+    base = acc * f.heads_q;
+  }
+  const int64_t start = base + (int64_t)hq * sk * ds_pitch(sq);
+  const int64_t cap = (p.ds_workspace_bytes - 1024) / 2;
+  return (start + (int64_t)sk * ds_pitch(sq) <= cap) ? start : -1;
+}
+
 
 // ---------------------------------------------------------------------------
 // dK / dV: each wave owns 32 keys (lane axis of S = Q K^T).
@@ -192,6 +220,21 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
       }
     };
 
+    // dS row of this lane's key in the score-gradient scratch, read back by
+    // dqs16_kernel (ds_on: this query head's dS is stored; wave-uniform).
+    // Lanes past the last key write to the scratch's slack instead, so every
+    // wave of a storing step issues the same stores (the end-of-step wait
+    // below counts them).
+    bool ds_on = false;
+    S* dsn = nullptr;
+    S* ds_dump = nullptr;
+    if (p.ds_workspace != nullptr) {
+      const int64_t region = ds_region(p, b, hq, sq, sk);
+      ds_on = region >= 0;
+      S* const ws = reinterpret_cast<S*>(p.ds_workspace);
+      dsn = ws + (ds_on ? region : 0) + (int64_t)n * ds_pitch(sq);
+      ds_dump = ws + (p.ds_workspace_bytes - 1024) / 2;
+    }
     const VisBounds kvb = key_block_bounds(md, n0w, ncols);
     // Visible rows of this lane's key, relative to the row of slot 0.
     int rlo, rhi;
@@ -314,9 +357,35 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
             dk[db] = EL::mma(tr_op_rowmap<D>(Qs, 0, 32 * db, j, lane), sb[j], dk[db]);
           }
         if constexpr (MODE == 0) sched_read_ahead<2 * C::NPV * C::NDB, 4, 2>();
+        if (t + 1 < my_count) store_stage(st ^ 1, m0 + C::BMQ);
+        if (ds_on) {
+          // Operand j of lane half h holds rows 16j + 4h + e and
+          // 16j + 8 + 4h + e (e < 4) of this lane's key.  One permlane32
+          // swap per dword gives half h rows 16h .. 16h + 15 (operand 0 of
+          // half 1 trades with operand 1 of half 0): 32 contiguous bytes of
+          // the dS row, two 16-byte stores.  Issued after the stage's
+          // register loads are consumed (a wait for those would also wait
+          // for these stores).
+          static_assert(C::NPV == 2, "one 32-row query step per dS store");
+          u32x4 w0 = __builtin_bit_cast(u32x4, sb[0]), w1 = __builtin_bit_cast(u32x4, sb[1]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const auto r = __builtin_amdgcn_permlane32_swap(w0[i], w1[i], false, false);
+            w0[i] = r[0];
+            w1[i] = r[1];
+          }
+          S* const at = (FA_DS_DUMP || !nvalid) ? ds_dump : dsn + m0 + 16 * h;
+          *reinterpret_cast<u32x4*>(at) = u32x4{w0[0], w0[1], w1[0], w1[1]};
+          *reinterpret_cast<u32x4*>(at + 8) = u32x4{w0[2], w0[3], w1[2], w1[3]};
+        }
+      } else if (t + 1 < my_count) {
+        store_stage(st ^ 1, m0 + C::BMQ);
       }
-      if (t + 1 < my_count) store_stage(st ^ 1, m0 + C::BMQ);
-      wait_vm_all();
+      // The next stage's loads must have landed; this step's dS stores,
+      // issued after them, may still be in flight (vector memory operations
+      // complete in issue order, so vmcnt <= #stores covers the loads).
+      if (ds_on && vis) wait_vm<2>();
+      else wait_vm_all();
       __syncthreads();
     }
   }
@@ -660,6 +729,173 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
       s16x4 w;
 #pragma unroll
       for (int r = 0; r < 4; ++r) w[r] = (short)EL::from_f(dq[db][4 * gq + r] * sc);
+      *reinterpret_cast<s16x4*>(dqr + db * 32 + 8 * gq + 4 * h) = w;
+    }
+}
+
+
+// ---------------------------------------------------------------------------
+// dQ from stored dS: dQ = scale * dS K.  The dK/dV pass stores the 16-bit dS
+// it forms (the operand of its dK product) in key-major rows of the scratch;
+// this kernel is the one remaining matrix product, block-sparse over the
+// visible tiles, in place of dq16_kernel's recomputation of S and dP.
+// A workgroup owns 128 query rows (32 per wave of a half) and splits their
+// key tiles in two halves of 4 waves, like dq16_kernel.  Per 64-key tile the
+// K rows and the dS rows of the tile's keys (128 queries each) go HBM -> LDS
+// by DMA; both MFMA operands are transposing LDS reads (the contracted index,
+// keys, runs along the tile rows of both).
+// ---------------------------------------------------------------------------
+template <int D>
+struct Dqs16Cfg {
+  static constexpr int NQ = 4;
+  static constexpr int NW = 2 * NQ;
+  static constexpr int NT = 64 * NW;
+  static constexpr int NTH = 64 * NQ;
+  static constexpr int BM = 32 * NQ;
+  static constexpr int BN = 64;
+  static constexpr int KT = BN * D;                // K tile (elements)
+  static constexpr int ST = BN * BM;               // dS tile: BN keys x BM queries
+  static constexpr int STAGE = KT + ST;
+  static constexpr int HALF = 2 * STAGE;
+  static constexpr int LOOP_BYTES = 2 * HALF * 2;
+  static constexpr int MERGE_BYTES = NQ * (D / 32) * 16 * 64 * 4;
+  static constexpr int LDS_BYTES = LOOP_BYTES > MERGE_BYTES ? LOOP_BYTES : MERGE_BYTES;
+  static constexpr int NPV = BN / 16;
+  static constexpr int NDB = D / 32;
+};
+
+template <typename Tag, int D>
+__global__ __launch_bounds__(512, 1) void dqs16_kernel(fa_bwd_params p, int num_m_blocks, float dq_scale) {
+  using C = Dqs16Cfg<D>;
+  using EL = Elem<Tag>;
+  using S = uint16_t;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  S* smem = reinterpret_cast<S*>(smem_raw);
+  const fa_fwd_params& f = p.fwd;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave8 = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int khalf = wave8 / C::NQ;
+  const int wave = wave8 % C::NQ;
+  const int htid = tid % C::NTH;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int bh_count = f.batch * f.heads_q;
+  const int mb_rev = blockIdx.x / bh_count;
+  const int bh = blockIdx.x - mb_rev * bh_count;
+  const int b = bh / f.heads_q, hq = bh - b * f.heads_q;
+  const int hk = hq / (f.heads_q / f.heads_kv);
+  const int mblk = num_m_blocks - 1 - mb_rev;  // heaviest causal blocks first
+
+  int q_start = 0, sq = f.seqlen_q, k_start = 0, sk = f.seqlen_k;
+  if (f.cu_seqlens_q) {
+    bounded_seq(f.cu_seqlens_q, b, f.total_q, q_start, sq);
+    bounded_seq(f.cu_seqlens_k, b, f.total_k, k_start, sk);
+  }
+  const int m0 = mblk * C::BM;
+  if (m0 >= sq) return;
+  const int64_t region = ds_region(p, b, hq, sq, sk);
+  const int64_t pitch = ds_pitch(sq);
+
+  const S* kbase = reinterpret_cast<const S*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1] +
+                   (int64_t)k_start * f.k_stride[2];
+  const S* dsbase = reinterpret_cast<const S*>(p.ds_workspace) + (region < 0 ? 0 : region) + m0;
+  const int64_t ks = f.k_stride[2];
+  const Mods md = make_mods(f, b, hq, sq, sk);
+
+  const int mlast = min(m0 + C::BM, sq) - 1;
+  int lo = 0, hi = sk;
+  if (f.causal) hi = min(hi, mlast + md.off + 1);
+  if (f.window_right >= 0) hi = min(hi, mlast + md.off + f.window_right + 1);
+  if (f.window_left >= 0) lo = max(0, m0 + md.off - f.window_left);
+  lo = lo / C::BN * C::BN;
+  const int ntiles = (hi > lo && region >= 0) ? (hi - lo + C::BN - 1) / C::BN : 0;
+
+  const int m0w = m0 + 32 * wave;
+  const int mrows = min(32, sq - m0w);
+  const int m = m0w + l32;
+  const bool mvalid = m < sq;
+
+  f32x16 dq[C::NDB];
+#pragma unroll
+  for (int i = 0; i < C::NDB; ++i) dq[i] = zero16();
+
+  DmaSwzTile<C::BN, D, C::NTH> kd;
+  DmaSwzTile<C::BN, C::BM, C::NTH> sd;
+  kd.init(ks, htid);
+  sd.init(pitch, htid);
+  const int nh0 = (ntiles + 1) / 2;
+  const int my_first = khalf == 0 ? 0 : nh0;
+  const int my_count = khalf == 0 ? nh0 : ntiles - nh0;
+  S* const hsmem = smem + khalf * C::HALF;
+  const uint32_t lds0 = lds_addr(hsmem);
+  auto load_stage = [&](int n0, int st) {
+    const int rows = min(C::BN, sk - n0);
+    const uint32_t base = lds0 + (uint32_t)(st * C::STAGE) * 2u;
+    kd.load(rows_rsrc_words<D>(kbase + (int64_t)n0 * ks, ks, rows), base, wave);
+    sd.load(rows_rsrc_words<C::BM>(dsbase + (int64_t)n0 * pitch, pitch, rows), base + C::KT * 2u, wave);
+  };
+
+  // Visible keys of this lane's row: partly visible tiles zero the dS of
+  // hidden pairs, which the dK/dV pass may not have written.
+  int klo, khi;
+  key_bounds(md, m, klo, khi);
+  const VisBounds qvb = row_block_bounds(md, m0w, mrows);
+  if (my_count > 0) load_stage(lo + my_first * C::BN, 0);
+  wait_vm_all();
+  __syncthreads();
+  for (int t = 0; t < nh0; ++t) {
+    const int n0 = lo + (my_first + t) * C::BN;
+    const int st = t & 1;
+    if (t + 1 < my_count) load_stage(n0 + C::BN, st ^ 1);
+    const int vis = t < my_count ? bounds_vis(qvb, n0, n0 + C::BN - 1) : 0;
+    if (vis) {
+      const S* Ks = hsmem + st * C::STAGE;
+      const S* Ss = Ks + C::KT;
+      s16x8 sb[C::NPV];
+#pragma unroll
+      for (int j = 0; j < C::NPV; ++j) sb[j] = tr_op_rowmap<C::BM>(Ss, 0, 32 * wave, j, lane);
+      if (vis == 1) {
+        // Element e of operand j holds key 32 (j/2) + 16 (j%2) + 4h + e%4
+        // (+ 8 for e >= 4), the row map of tr_op_rowmap.
+        const Span ks2 = make_span(klo, khi, n0 + 4 * h);
+#pragma unroll
+        for (int j = 0; j < C::NPV; ++j)
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (!in_span(ks2, 32 * (j >> 1) + 16 * (j & 1) + 8 * (e >> 2) + (e & 3))) sb[j][e] = 0;
+      }
+#pragma unroll
+      for (int j = 0; j < C::NPV; ++j)
+#pragma unroll
+        for (int db = 0; db < C::NDB; ++db) dq[db] = EL::mma(tr_op_rowmap<D>(Ks, 0, 32 * db, j, lane), sb[j], dq[db]);
+    }
+    wait_vm_all();
+    __syncthreads();
+  }
+
+  // dQ = dQ(first key half) + dQ(second key half), summed in that order.
+  {
+    float* ow = reinterpret_cast<float*>(smem_raw);
+    if (khalf == 1) {
+#pragma unroll
+      for (int db = 0; db < C::NDB; ++db) park_acc(ow + (wave * C::NDB + db) * 1024, lane, dq[db]);
+    }
+    __syncthreads();
+    if (khalf == 1) return;
+#pragma unroll
+    for (int db = 0; db < C::NDB; ++db) dq[db] += unpark_acc(ow + (wave * C::NDB + db) * 1024, lane);
+  }
+
+  if (!mvalid) return;
+  S* dqr = reinterpret_cast<S*>(p.dq) + b * p.dq_stride[0] + hq * p.dq_stride[1] +
+           (int64_t)(q_start + m) * p.dq_stride[2];
+#pragma unroll
+  for (int db = 0; db < C::NDB; ++db)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      s16x4 w;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[r] = (short)EL::from_f(dq[db][4 * gq + r] * dq_scale);
       *reinterpret_cast<s16x4*>(dqr + db * 32 + 8 * gq + 4 * h) = w;
     }
 }

@@ -555,6 +555,18 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(fa_bwd_params p, int num_m_
 
 // ---------------------------------------------------------------------------
 template <typename Tag, int D, int MODE>
+static hipError_t run_bwd_dkdv16(const fa_bwd_params& p, hipStream_t stream) {
+  using C = Dkdv16Cfg<D>;
+  auto kern = dkdv16_kernel<Tag, D, MODE>;
+  hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
+  if (e != hipSuccess) return e;
+  const int nnb = (p.fwd.seqlen_k + C::BN - 1) / C::BN;
+  const long grid = (long)nnb * p.fwd.batch * p.fwd.heads_kv;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nnb);
+  return hipGetLastError();
+}
+
+template <typename Tag, int D, int MODE>
 static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream) {
   const fa_fwd_params& f = p.fwd;
   constexpr bool FAST = !std::is_same<Tag, f32_t>::value && D <= 128;
@@ -562,9 +574,17 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
   if constexpr (FAST)
     fast_ok = buf_rows_ok(f.q_stride[2], Dkdv16Cfg<D>::BMQ) && buf_rows_ok(p.dout_stride[2], Dkdv16Cfg<D>::BMQ) &&
               buf_rows_ok(f.k_stride[2], Dq16Cfg<D>::BN) && buf_rows_ok(f.v_stride[2], Dq16Cfg<D>::BN);
-  // The full 16-bit backward computes delta inside the dQ kernel, which then
-  // runs first; otherwise delta has its own kernel.
-  const bool fused_delta = fast_ok && (phases & 1) && (phases & 4);
+  // With score-gradient scratch the dK/dV kernel stores dS and dQ = dS K
+  // runs after it (dqs16_kernel); without it, the full 16-bit backward
+  // computes delta inside the dQ kernel, which then runs first.  Otherwise
+  // delta has its own kernel.
+  bool use_ds = false;
+  if constexpr (FAST) {
+    const size_t need = bwd_ds_bytes(p);
+    use_ds = fast_ok && p.ds_workspace != nullptr && need > 0 && p.ds_workspace_bytes >= (int64_t)need &&
+             buf_rows_ok(ds_pitch(f.seqlen_q), Dqs16Cfg<D>::BN);
+  }
+  const bool fused_delta = fast_ok && !use_ds && (phases & 1) && (phases & 4);
   if ((phases & 1) && !fused_delta) {
     dim3 grid((f.seqlen_q + 15) / 16, f.batch * f.heads_q);
     hipLaunchKernelGGL((bwd_delta_kernel<Tag, D>), grid, dim3(256), 0, stream, p);
@@ -573,7 +593,26 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
   }
   if constexpr (FAST) {
   if (fast_ok) {
-    if (phases & 4) {
+    if ((phases & 4) && use_ds) {
+      // dQ from the dS the dK/dV pass stored: runs after it.
+      if (phases & 2) {
+        hipError_t e = run_bwd_dkdv16<Tag, D, MODE>(p, stream);
+        if (e != hipSuccess) return e;
+        phases &= ~2;
+      }
+      using C = Dqs16Cfg<D>;
+      auto kern = dqs16_kernel<Tag, D>;
+      hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
+      if (e != hipSuccess) return e;
+      const int nmb = (f.seqlen_q + C::BM - 1) / C::BM;
+      const long grid = (long)nmb * f.batch * f.heads_q;
+      // MODE 3 stores dS / 4 (its softcap factor is (1 - tanh^2) / 4).
+      const float dq_scale = f.softmax_scale * (MODE == 3 ? 4.f : 1.f);
+      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb, dq_scale);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    if ((phases & 4) && !use_ds) {
       using C = Dq16Cfg<D>;
       auto kern = dq16_kernel<Tag, D, MODE>;
       hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
@@ -585,14 +624,11 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
       if (e != hipSuccess) return e;
     }
     if (phases & 2) {
-      using C = Dkdv16Cfg<D>;
-      auto kern = dkdv16_kernel<Tag, D, MODE>;
-      hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
-      if (e != hipSuccess) return e;
-      const int nnb = (f.seqlen_k + C::BN - 1) / C::BN;
-      const long grid = (long)nnb * f.batch * f.heads_kv;
-      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nnb);
-      e = hipGetLastError();
+      // Without dS scratch the kernel must not store dS (ds_workspace is
+      // only honoured when its size was checked above).
+      fa_bwd_params q = p;
+      if (!use_ds) q.ds_workspace = nullptr;
+      hipError_t e = run_bwd_dkdv16<Tag, D, MODE>(q, stream);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -13,7 +13,7 @@ import threading
 
 import torch
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 DTYPE_CODE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
 _LIB_NAME = "libfa_mi355x.so"
@@ -53,6 +53,7 @@ class BwdParams(ctypes.Structure):
         ("dv", ctypes.c_void_p), ("delta", ctypes.c_void_p),
         ("dout_stride", _i64_4), ("dq_stride", _i64_4), ("dk_stride", _i64_4),
         ("dv_stride", _i64_4), ("delta_stride", _i64_3),
+        ("ds_workspace", ctypes.c_void_p), ("ds_workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -120,7 +121,7 @@ _STRUCTS = (FwdParams, BwdParams, DecodeParams, PagedParams, TinyParams, AppendP
 EXPORTS = (
     "fa_abi_version", "fa_last_error_string", "fa_params_size", "fa_decode_workspace_bytes",
     "fa_decode_ticket_count",
-    "fa_fwd", "fa_bwd", "fa_bwd_phase", "fa_decode_splitk", "fa_decode_splitk_noalloc", "fa_decode_paged",
+    "fa_fwd", "fa_bwd", "fa_bwd_phase", "fa_bwd_workspace_bytes", "fa_decode_splitk", "fa_decode_splitk_noalloc", "fa_decode_paged",
     "fa_tiny_fwd_f32",
     "fa_kvcache_append",
 )
@@ -153,6 +154,8 @@ def lib():
         handle.fa_params_size.argtypes = [ctypes.c_int]
         handle.fa_decode_workspace_bytes.restype = ctypes.c_size_t
         handle.fa_decode_workspace_bytes.argtypes = [ctypes.c_int] * 5
+        handle.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
+        handle.fa_bwd_workspace_bytes.argtypes = [ctypes.c_void_p]
         handle.fa_decode_ticket_count.restype = ctypes.c_size_t
         handle.fa_decode_ticket_count.argtypes = [ctypes.c_int] * 3
         for name, struct in (("fa_fwd", FwdParams), ("fa_bwd", BwdParams),
@@ -197,6 +200,24 @@ def call(name, params, device_tensor):
 
 def call_bwd_phase(params, phase, device_tensor):
     _check(lib().fa_bwd_phase(ctypes.byref(params), int(phase), _stream(device_tensor)), "fa_bwd_phase")
+
+
+# Largest score-gradient scratch the backward allocates; above it dQ
+# recomputes the scores instead of reading the stored dS.
+DS_SCRATCH_LIMIT_BYTES = 8 << 30
+
+
+def attach_ds_scratch(params, device_tensor):
+    """Give a filled BwdParams the dS scratch its backward can use (dQ as
+    the single product dS K).  Returns the scratch tensor, which must stay
+    alive until the launch is done, or None when the path does not apply."""
+    need = int(lib().fa_bwd_workspace_bytes(ctypes.byref(params)))
+    if need == 0 or need > DS_SCRATCH_LIMIT_BYTES:
+        params.ds_workspace, params.ds_workspace_bytes = None, 0
+        return None
+    buf = torch.empty(need, dtype=torch.uint8, device=device_tensor.device)
+    params.ds_workspace, params.ds_workspace_bytes = buf.data_ptr(), need
+    return buf
 
 
 def decode_workspace_bytes(batch, heads_q, seqlen_q, head_dim, num_splits):

@@ -257,7 +257,8 @@ def _bwd_setup(dout, query, key, value, out, lse, causal, softmax_scale, window,
     for name, t in (("dout_stride", do), ("dq_stride", dq), ("dk_stride", dk), ("dv_stride", dv)):
         _set(getattr(params, name), _native.strides(t))
     _set(params.delta_stride, [s if n > 1 else 0 for s, n in zip(delta.stride(), delta.shape)])
-    keep = (q, k, v, o, do, lse, delta, bias_t, alibi_t)
+    ds = _native.attach_ds_scratch(params, query)
+    keep = (q, k, v, o, do, lse, delta, bias_t, alibi_t, ds)
     return params, dq, dk, dv, keep
 
 
@@ -699,6 +700,7 @@ def _backward_varlen(dout, query, key, value, out, lse, cu_seqlens_q, cu_seqlens
         st = _native.strides(t)
         _set(getattr(params, name), (0, st[1], t.stride(0), 1))
     _set(params.delta_stride, (0, delta.stride(0), delta.stride(1)))
+    _ds = _native.attach_ds_scratch(params, query)
     _native.call("fa_bwd", params, query)
     if kdim != head_dim:
         dq, dk, dv = dq[..., :head_dim], dk[..., :head_dim], dv[..., :head_dim]

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 3
+#define FA_ABI_VERSION 4
 
 typedef enum fa_dtype {
   FA_DTYPE_F16 = 0,
@@ -121,6 +121,15 @@ typedef struct fa_bwd_params {
   int64_t dk_stride[4];
   int64_t dv_stride[4];
   int64_t delta_stride[3];
+  /* Optional score-gradient scratch (no counterpart in the reference, whose
+   * dQ kernel recomputes the scores).  When non-NULL and at least
+   * fa_bwd_workspace_bytes(params) bytes, the dK/dV pass stores the 16-bit
+   * dS it already forms and dQ becomes the single product dS K, instead of
+   * recomputing S and dP (two of its three matrix products).  NULL, or a
+   * configuration fa_bwd_workspace_bytes returns 0 for: dQ recomputes.
+   * Results agree either way to the rounding of the accumulation order. */
+  void* ds_workspace;
+  int64_t ds_workspace_bytes;
 } fa_bwd_params;
 
 /*
@@ -308,6 +317,12 @@ int fa_bwd(const fa_bwd_params* params, void* stream);
  * Triton calls, interface.py:226/:236/:258); it exists so profilers and
  * benchmarks can time each backward kernel on its own. */
 int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream);
+/* Bytes of ds_workspace the backward of `params` can use (0: the dS path
+ * does not apply: fp32, head_dim > 128, or more than 512 varlen sequences).
+ * Dense: batch * heads_q * Sk * round_up(Sq, 32) * 2 plus 1 KiB; varlen, an
+ * upper bound from max_seqlen_k and total_q.  With dS scratch, phase 2 of
+ * fa_bwd_phase reads the dS that phase 1 stored. */
+size_t fa_bwd_workspace_bytes(const fa_bwd_params* params);
 /* uint32 counters `tickets` needs: batch * heads_q * seqlen_q. */
 size_t fa_decode_ticket_count(int batch, int heads_q, int seqlen_q);
 
