@@ -18,8 +18,8 @@
 #include "fa_internal.hpp"
 #include "fa_tiles.hpp"
 
-#ifndef FA_DS_DUMP
-#define FA_DS_DUMP 0
+#ifndef FA_DS_NT
+#define FA_DS_NT 1
 #endif
 
 namespace fa {
@@ -33,20 +33,20 @@ __device__ inline int64_t ds_region(const fa_bwd_params& p, int b, int hq, int s
   const fa_fwd_params& f = p.fwd;
   int64_t base;
   if (!f.cu_seqlens_q) {
-    base = (int64_t)b * f.heads_q * sk * ds_pitch(sq);
+    base = (int64_t)b * f.heads_q * ds_region_elems(sq, sk);
   } else {
     int64_t acc = 0;
     for (int i = 0; i < b; ++i) {
       int s0, l0, s1, l1;
       bounded_seq(f.cu_seqlens_q, i, f.total_q, s0, l0);
       bounded_seq(f.cu_seqlens_k, i, f.total_k, s1, l1);
-      acc += (int64_t)l1 * ds_pitch(l0);
+      acc += ds_region_elems(l0, l1);
     }
     base = acc * f.heads_q;
   }
-  const int64_t start = base + (int64_t)hq * sk * ds_pitch(sq);
+  const int64_t start = base + (int64_t)hq * ds_region_elems(sq, sk);
   const int64_t cap = (p.ds_workspace_bytes - 1024) / 2;
-  return (start + (int64_t)sk * ds_pitch(sq) <= cap) ? start : -1;
+  return (start + ds_region_elems(sq, sk) <= cap) ? start : -1;
 }
 
 
@@ -232,7 +232,9 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
       const int64_t region = ds_region(p, b, hq, sq, sk);
       ds_on = region >= 0;
       S* const ws = reinterpret_cast<S*>(p.ds_workspace);
-      dsn = ws + (ds_on ? region : 0) + (int64_t)n * ds_pitch(sq);
+      // row n % 64 of the key block's tiles; + (query block) * tile + m % 128
+      dsn = ws + (ds_on ? region : 0) + (int64_t)(n / kDsTileKeys) * ds_qblocks(sq) * kDsTileElems +
+            (n % kDsTileKeys) * kDsTileQueries;
       ds_dump = ws + (p.ds_workspace_bytes - 1024) / 2;
     }
     const VisBounds kvb = key_block_bounds(md, n0w, ncols);
@@ -374,9 +376,15 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
             w0[i] = r[0];
             w1[i] = r[1];
           }
-          S* const at = (FA_DS_DUMP || !nvalid) ? ds_dump : dsn + m0 + 16 * h;
-          *reinterpret_cast<u32x4*>(at) = u32x4{w0[0], w0[1], w1[0], w1[1]};
-          *reinterpret_cast<u32x4*>(at + 8) = u32x4{w0[2], w0[3], w1[2], w1[3]};
+          S* const at = !nvalid ? ds_dump
+                                : dsn + (int64_t)(m0 / kDsTileQueries) * kDsTileElems + (m0 % kDsTileQueries) + 16 * h;
+          if (FA_DS_NT) {
+            __builtin_nontemporal_store(u32x4{w0[0], w0[1], w1[0], w1[1]}, reinterpret_cast<u32x4*>(at));
+            __builtin_nontemporal_store(u32x4{w0[2], w0[3], w1[2], w1[3]}, reinterpret_cast<u32x4*>(at + 8));
+          } else {
+            *reinterpret_cast<u32x4*>(at) = u32x4{w0[0], w0[1], w1[0], w1[1]};
+            *reinterpret_cast<u32x4*>(at + 8) = u32x4{w0[2], w0[3], w1[2], w1[3]};
+          }
         }
       } else if (t + 1 < my_count) {
         store_stage(st ^ 1, m0 + C::BMQ);
@@ -745,6 +753,16 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
 // by DMA; both MFMA operands are transposing LDS reads (the contracted index,
 // keys, runs along the tile rows of both).
 // ---------------------------------------------------------------------------
+#ifndef FA_DQS_BN
+#define FA_DQS_BN 32
+#endif
+#ifndef FA_DQS_EXP
+#define FA_DQS_EXP 0
+#endif
+
+#ifndef FA_DQS_STAGES
+#define FA_DQS_STAGES 4
+#endif
 template <int D>
 struct Dqs16Cfg {
   static constexpr int NQ = 4;
@@ -752,16 +770,20 @@ struct Dqs16Cfg {
   static constexpr int NT = 64 * NW;
   static constexpr int NTH = 64 * NQ;
   static constexpr int BM = 32 * NQ;
-  static constexpr int BN = 64;
-  static constexpr int KT = BN * D;                // K tile (elements)
-  static constexpr int ST = BN * BM;               // dS tile: BN keys x BM queries
+  static constexpr int BN = FA_DQS_BN;             // keys per step (half a dS tile)
+  static constexpr int NSTG = FA_DQS_STAGES;       // ring of stages per key half
+  static constexpr int KT = BN * D;                // K rows (elements)
+  static constexpr int ST = BN * BM;               // dS rows: BN keys x BM queries
   static constexpr int STAGE = KT + ST;
-  static constexpr int HALF = 2 * STAGE;
+  static constexpr int HALF = NSTG * STAGE;
   static constexpr int LOOP_BYTES = 2 * HALF * 2;
   static constexpr int MERGE_BYTES = NQ * (D / 32) * 16 * 64 * 4;
   static constexpr int LDS_BYTES = LOOP_BYTES > MERGE_BYTES ? LOOP_BYTES : MERGE_BYTES;
   static constexpr int NPV = BN / 16;
   static constexpr int NDB = D / 32;
+  // DMA instructions per thread per stage (the end-of-step wait counts them)
+  static constexpr int LOADS = (KT / 8) / NTH + (ST / 8) / NTH;
+  static_assert(BM == kDsTileQueries && kDsTileKeys % BN == 0, "a dQ step reads whole rows of one dS tile");
 };
 
 template <typename Tag, int D>
@@ -794,11 +816,13 @@ __global__ __launch_bounds__(512, 1) void dqs16_kernel(fa_bwd_params p, int num_
   const int m0 = mblk * C::BM;
   if (m0 >= sq) return;
   const int64_t region = ds_region(p, b, hq, sq, sk);
-  const int64_t pitch = ds_pitch(sq);
+  const int64_t qblocks = ds_qblocks(sq);
 
   const S* kbase = reinterpret_cast<const S*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1] +
                    (int64_t)k_start * f.k_stride[2];
-  const S* dsbase = reinterpret_cast<const S*>(p.ds_workspace) + (region < 0 ? 0 : region) + m0;
+  // dS tiles of this query block: key block kb at dsbase + kb * qblocks * tile
+  const S* dsbase = reinterpret_cast<const S*>(p.ds_workspace) + (region < 0 ? 0 : region) +
+                    (int64_t)mblk * kDsTileElems;
   const int64_t ks = f.k_stride[2];
   const Mods md = make_mods(f, b, hq, sq, sk);
 
@@ -822,17 +846,21 @@ __global__ __launch_bounds__(512, 1) void dqs16_kernel(fa_bwd_params p, int num_
   DmaSwzTile<C::BN, D, C::NTH> kd;
   DmaSwzTile<C::BN, C::BM, C::NTH> sd;
   kd.init(ks, htid);
-  sd.init(pitch, htid);
+  sd.init(C::BM, htid);
   const int nh0 = (ntiles + 1) / 2;
   const int my_first = khalf == 0 ? 0 : nh0;
   const int my_count = khalf == 0 ? nh0 : ntiles - nh0;
   S* const hsmem = smem + khalf * C::HALF;
   const uint32_t lds0 = lds_addr(hsmem);
+  // Stage st holds step t with t % NSTG == st; NSTG - 1 steps are in flight
+  // while one is computed.
   auto load_stage = [&](int n0, int st) {
     const int rows = min(C::BN, sk - n0);
     const uint32_t base = lds0 + (uint32_t)(st * C::STAGE) * 2u;
     kd.load(rows_rsrc_words<D>(kbase + (int64_t)n0 * ks, ks, rows), base, wave);
-    sd.load(rows_rsrc_words<C::BM>(dsbase + (int64_t)n0 * pitch, pitch, rows), base + C::KT * 2u, wave);
+    const S* drows = dsbase + (int64_t)(n0 / kDsTileKeys) * qblocks * kDsTileElems + (n0 % kDsTileKeys) * C::BM;
+    if (FA_DQS_EXP != 2) sd.load(rows_rsrc_words<C::BM>(drows, C::BM, rows), base + C::KT * 2u, wave);
+    else kd.load(rows_rsrc_words<D>(kbase + (int64_t)n0 * ks, ks, rows), base + C::KT * 2u, wave);
   };
 
   // Visible keys of this lane's row: partly visible tiles zero the dS of
@@ -840,15 +868,23 @@ __global__ __launch_bounds__(512, 1) void dqs16_kernel(fa_bwd_params p, int num_
   int klo, khi;
   key_bounds(md, m, klo, khi);
   const VisBounds qvb = row_block_bounds(md, m0w, mrows);
-  if (my_count > 0) load_stage(lo + my_first * C::BN, 0);
-  wait_vm_all();
-  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < C::NSTG - 1; ++i)
+    if (i < my_count) load_stage(lo + (my_first + i) * C::BN, i);
   for (int t = 0; t < nh0; ++t) {
     const int n0 = lo + (my_first + t) * C::BN;
-    const int st = t & 1;
-    if (t + 1 < my_count) load_stage(n0 + C::BN, st ^ 1);
+    const int st = t % C::NSTG;
+    // Step t's loads have landed once at most the later steps' loads are
+    // outstanding (vector memory operations complete in issue order).
+    const int later = min(my_count - 1 - t, C::NSTG - 2);
+    if (later >= 2) wait_vm<2 * C::LOADS>();
+    else if (later == 1) wait_vm<C::LOADS>();
+    else wait_vm_all();
+    __syncthreads();
+    // The stage refilled here was last read in step t - 1, before the barrier.
+    if (t + C::NSTG - 1 < my_count) load_stage(n0 + (C::NSTG - 1) * C::BN, (t + C::NSTG - 1) % C::NSTG);
     const int vis = t < my_count ? bounds_vis(qvb, n0, n0 + C::BN - 1) : 0;
-    if (vis) {
+    if (vis && FA_DQS_EXP != 1) {
       const S* Ks = hsmem + st * C::STAGE;
       const S* Ss = Ks + C::KT;
       s16x8 sb[C::NPV];
@@ -869,9 +905,8 @@ __global__ __launch_bounds__(512, 1) void dqs16_kernel(fa_bwd_params p, int num_
 #pragma unroll
         for (int db = 0; db < C::NDB; ++db) dq[db] = EL::mma(tr_op_rowmap<D>(Ks, 0, 32 * db, j, lane), sb[j], dq[db]);
     }
-    wait_vm_all();
-    __syncthreads();
   }
+  __syncthreads();
 
   // dQ = dQ(first key half) + dQ(second key half), summed in that order.
   {

@@ -579,10 +579,9 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
   // computes delta inside the dQ kernel, which then runs first.  Otherwise
   // delta has its own kernel.
   bool use_ds = false;
-  if constexpr (FAST) {
+  if constexpr (FAST && D >= 64) {
     const size_t need = bwd_ds_bytes(p);
-    use_ds = fast_ok && p.ds_workspace != nullptr && need > 0 && p.ds_workspace_bytes >= (int64_t)need &&
-             buf_rows_ok(ds_pitch(f.seqlen_q), Dqs16Cfg<D>::BN);
+    use_ds = fast_ok && p.ds_workspace != nullptr && need > 0 && p.ds_workspace_bytes >= (int64_t)need;
   }
   const bool fused_delta = fast_ok && !use_ds && (phases & 1) && (phases & 4);
   if ((phases & 1) && !fused_delta) {
@@ -593,6 +592,7 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
   }
   if constexpr (FAST) {
   if (fast_ok) {
+    if constexpr (D >= 64) {
     if ((phases & 4) && use_ds) {
       // dQ from the dS the dK/dV pass stored: runs after it.
       if (phases & 2) {
@@ -611,6 +611,7 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
       hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb, dq_scale);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
+    }
     }
     if ((phases & 4) && !use_ds) {
       using C = Dq16Cfg<D>;

@@ -31,12 +31,17 @@ hipError_t launch_append(const fa_append_params& p, hipStream_t stream);
 size_t decode_workspace_bytes(int batch, int heads_q, int seqlen_q, int head_dim, int num_splits);
 
 // Score-gradient scratch of the 16-bit backward: per (sequence, query head)
-// a region of Sk rows (keys) of ds_pitch(Sq) 16-bit dS values (queries), the
-// regions of a varlen batch packed in sequence order.  Rows are padded to 32
-// queries (a dK/dV query step) and the scratch ends in 1 KiB of slack that a
-// dQ tile reaching past the last row may read.
+// a region of tiles of 64 keys x 128 queries (16 KiB of 16-bit dS, key-major
+// rows of 128 queries), tile (key block kb, query block qb) at
+// kb * ds_qblocks(Sq) + qb; the regions of a varlen batch are packed in
+// sequence order.  A dQ tile then reads 16 contiguous KiB.  The scratch ends
+// in 1 KiB of slack where lanes past the last key of a dK/dV wave write.
 constexpr int kDsMaxVarlenBatch = 512;
-__host__ __device__ inline int64_t ds_pitch(int sq) { return ((int64_t)sq + 31) / 32 * 32; }
+constexpr int kDsTileKeys = 64, kDsTileQueries = 128, kDsTileElems = kDsTileKeys * kDsTileQueries;
+__host__ __device__ inline int64_t ds_qblocks(int sq) { return ((int64_t)sq + kDsTileQueries - 1) / kDsTileQueries; }
+__host__ __device__ inline int64_t ds_region_elems(int sq, int sk) {
+  return ((int64_t)sk + kDsTileKeys - 1) / kDsTileKeys * ds_qblocks(sq) * kDsTileElems;
+}
 size_t bwd_ds_bytes(const fa_bwd_params& p);
 
 // Raise a kernel's dynamic LDS limit once per process (gfx950: 160 KiB/CU).

@@ -318,9 +318,10 @@ int fa_bwd(const fa_bwd_params* params, void* stream);
  * benchmarks can time each backward kernel on its own. */
 int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream);
 /* Bytes of ds_workspace the backward of `params` can use (0: the dS path
- * does not apply: fp32, head_dim > 128, or more than 512 varlen sequences).
- * Dense: batch * heads_q * Sk * round_up(Sq, 32) * 2 plus 1 KiB; varlen, an
- * upper bound from max_seqlen_k and total_q.  With dS scratch, phase 2 of
+ * does not apply: fp32, head_dim other than 64 or 128, or more than 512
+ * varlen sequences).
+ * Dense: batch * heads_q * ceil(Sk / 64) * ceil(Sq / 128) * 16 KiB plus
+ * 1 KiB; varlen, an upper bound from max_seqlen_k, total_q and batch.  With dS scratch, phase 2 of
  * fa_bwd_phase reads the dS that phase 1 stored. */
 size_t fa_bwd_workspace_bytes(const fa_bwd_params* params);
 /* uint32 counters `tickets` needs: batch * heads_q * seqlen_q. */
