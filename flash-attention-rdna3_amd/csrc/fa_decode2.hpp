@@ -133,8 +133,10 @@ __global__ __launch_bounds__((KV8 || PAGE == 2) ? 512 : 256) void decode2_kernel
   const int hq = hk * group + gq;
   // Last key this lane's query row sees (bottom-right causal), or all.
   const int klim = a.causal ? len - a.seqlen_q + mq : INT_MAX;
+  // Q operand: loaded after the first chunk's loads are issued (one round
+  // trip to memory for both), waited for at its first use.
   s16x8 qop[C::NSTEP];
-  {
+  auto load_q = [&]() {
     const S* qrow = reinterpret_cast<const S*>(a.q) + b * a.q_stride[0] + hq * a.q_stride[1] + mq * a.q_stride[2];
 #pragma unroll
     for (int s = 0; s < C::NSTEP; ++s) {
@@ -144,12 +146,9 @@ __global__ __launch_bounds__((KV8 || PAGE == 2) ? 512 : 256) void decode2_kernel
       const int d0 = C::KP ? 64 * (s / 2) + 16 * g4 + 8 * (s % 2) : 8 * (4 * s + g4);
       qop[s] = load_op<Tag>(qrow + d0);
     }
-    wait_vm_all();
-    if (!rvalid) {
 #pragma unroll
-      for (int s = 0; s < C::NSTEP; ++s) qop[s] = zero_op<Tag>();
-    }
-  }
+    for (int s = 0; s < C::NSTEP; ++s) qop[s] = rvalid ? qop[s] : zero_op<Tag>();
+  };
 
   const KE* kbase = reinterpret_cast<const KE*>(a.k);
   const KE* vbase = reinterpret_cast<const KE*>(a.v);
@@ -269,6 +268,20 @@ __global__ __launch_bounds__((KV8 || PAGE == 2) ? 512 : 256) void decode2_kernel
     }
   };
   auto compute_chunk = [&](int c, const KRaw (&kd)[2][C::KN], const VRaw (&vd)[C::VN]) {
+#ifdef FA_DEC_EXP
+    if constexpr (!KV8) {
+      uint32_t x = 0;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int s2 = 0; s2 < C::KN; ++s2) { const u32x4 w = __builtin_bit_cast(u32x4, kd[kb][s2]); x ^= w[0] ^ w[1] ^ w[2] ^ w[3]; }
+#pragma unroll
+      for (int i = 0; i < C::VN; ++i) { const u32x4 w = __builtin_bit_cast(u32x4, vd[i]); x ^= w[0] ^ w[1] ^ w[2] ^ w[3]; }
+      acc[0][0] += __uint_as_float(x & 0x3fffffffu) * 1e-30f;
+      l_i = 1.f; m_i = 0.f;
+      return;
+    }
+#endif
     const uint32_t vmask = chunk_mask(c);
     // V rows -> this wave's LDS tile (swizzled); the previous chunk's reads of
     // the tile precede these writes in the wave's LDS order.
@@ -353,7 +366,10 @@ __global__ __launch_bounds__((KV8 || PAGE == 2) ? 512 : 256) void decode2_kernel
   const int mine = cnt > wave ? (cnt - wave + C::NW - 1) / C::NW : 0;
   const int groups = (mine + C::NBUF - 1) / C::NBUF;
 #pragma unroll
-  for (int j = 0; j < C::NBUF; ++j) issue_chunk(c0 + wave + C::NW * j, j < mine, kr[j], vreg[j]);
+  for (int j = 0; j < C::NBUF; ++j) {
+    issue_chunk(c0 + wave + C::NW * j, j < mine, kr[j], vreg[j]);
+    if (j == 0) load_q();
+  }
   // Steady state: every slot is refilled after use.
   for (int gi = 0; gi + 1 < groups; ++gi) {
 #pragma unroll
