@@ -81,3 +81,22 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_native, "_lib", None)
     with pytest.raises(RuntimeError, match="native library not found"):
         _native.lib()
+
+
+def test_bwd_ds_workspace_size():
+    """fa_bwd_workspace_bytes: 64-key x 128-query tiles of 16-bit dS per
+    (batch, query head) plus 1 KiB; 0 where the dS path does not apply."""
+    lib = _native.lib()
+    p = _native.BwdParams()
+    p.fwd.abi_version, p.fwd.dtype = _native.ABI_VERSION, 0
+    p.fwd.batch, p.fwd.heads_q, p.fwd.heads_kv = 2, 16, 16
+    p.fwd.seqlen_q = p.fwd.seqlen_k = 2048
+    p.fwd.head_dim = 128
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(p)) == 2 * 16 * 32 * 16 * 16384 + 1024
+    p.fwd.seqlen_q, p.fwd.seqlen_k = 129, 65  # 2 query blocks x 2 key blocks
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(p)) == 2 * 16 * 4 * 16384 + 1024
+    p.fwd.head_dim = 32
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(p)) == 0
+    p.fwd.head_dim, p.fwd.dtype = 128, 2  # fp32
+    assert lib.fa_bwd_workspace_bytes(ctypes.byref(p)) == 0
+    assert lib.fa_bwd_workspace_bytes(None) == 0

@@ -1,0 +1,110 @@
+"""The dS-scratch backward (dK/dV stores dS, dQ = dS K) against the
+recompute backward (dQ recomputes S and dP), on the same inputs: dV comes
+from the same kernel and must match bit for bit; delta = rowsum(O dO) is
+summed in another order (its own kernel instead of inside dQ), which moves
+dK by rounding, and dQ differs in the accumulation order of its products, so
+both must agree to a few units of the output dtype's rounding.  Covers dense, GQA, windows, softcap (its dS is
+stored quartered), ALiBi, bias, dropout, cross shapes, head_dim 64 and varlen
+packing."""
+
+import pytest
+import torch
+
+from fa_rdna3 import _native, alibi_slopes, flash_attention, flash_attention_varlen
+
+pytestmark = pytest.mark.gpu
+DEVICE = "cuda"
+
+
+def _both(fn, *tensors):
+    def run():
+        leaves = [t.detach().clone().requires_grad_(True) for t in tensors[:3]]
+        out = fn(*leaves)
+        out.backward(tensors[3])
+        return out.detach(), [t.grad for t in leaves]
+
+    out_a, g_a = run()
+    saved = _native.DS_SCRATCH_LIMIT_BYTES
+    _native.DS_SCRATCH_LIMIT_BYTES = 0
+    try:
+        out_b, g_b = run()
+    finally:
+        _native.DS_SCRATCH_LIMIT_BYTES = saved
+    return out_a, g_a, out_b, g_b
+
+
+def _check(g_a, g_b, dtype):
+    dq_a, dk_a, dv_a = g_a
+    dq_b, dk_b, dv_b = g_b
+    assert torch.equal(dv_a, dv_b)
+    ulp = 2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7
+    for x, y in ((dq_a, dq_b), (dk_a, dk_b)):
+        scale = y.float().abs().max().item()
+        err = (x.float() - y.float()).abs().max().item()
+        assert torch.isfinite(x).all()
+        assert err <= 4 * ulp * max(scale, 1e-3), (err, scale)
+
+
+def _rand(shape, dtype):
+    return torch.randn(shape, device=DEVICE, dtype=dtype)
+
+
+CASES = [
+    dict(),
+    dict(causal=True),
+    dict(causal=True, window_size=(100, 0)),
+    dict(window_size=(64, 32)),
+    dict(causal=True, softcap=30.0),
+    dict(causal=True, softcap=30.0, window_size=(200, -1)),
+    dict(alibi=True),
+    dict(bias=True),
+    dict(dropout_p=0.2),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_dense_ds_path_matches_recompute(dtype, head_dim, case):
+    opts = dict(CASES[case])
+    torch.manual_seed(case * 7 + head_dim)
+    hq, hk, sq, sk = 8, 2, 300, 421
+    q, do = _rand((2, hq, sq, head_dim), dtype), _rand((2, hq, sq, head_dim), dtype)
+    k, v = _rand((2, hk, sk, head_dim), dtype), _rand((2, hk, sk, head_dim), dtype)
+    if opts.pop("alibi", False):
+        opts["alibi_slopes"] = alibi_slopes(hq, device=DEVICE)
+    if opts.pop("bias", False):
+        opts["bias"] = _rand((1, hq, sq, sk), dtype)
+    if "dropout_p" in opts:
+        # the same dropout seed for both runs: re-seed torch before each
+        gen_state = torch.get_rng_state()
+
+        def fn(a, b, c):
+            torch.set_rng_state(gen_state)
+            return flash_attention(a, b, c, **opts)
+    else:
+        def fn(a, b, c):
+            return flash_attention(a, b, c, **opts)
+    out_a, g_a, out_b, g_b = _both(fn, q, k, v, do)
+    assert torch.equal(out_a, out_b)
+    _check(g_a, g_b, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("opts", [dict(causal=True), dict(causal=True, window_size=(256, -1), softcap=50.0),
+                                  dict(causal=False)])
+def test_varlen_ds_path_matches_recompute(dtype, opts):
+    torch.manual_seed(5)
+    lengths = [1, 130, 7, 513, 64, 300]
+    total = sum(lengths)
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32, device=DEVICE)
+    q, do = _rand((total, 8, 128), dtype), _rand((total, 8, 128), dtype)
+    k, v = _rand((total, 2, 128), dtype), _rand((total, 2, 128), dtype)
+    mx = max(lengths)
+
+    def fn(a, b, c):
+        return flash_attention_varlen(a, b, c, cu, cu, mx, mx, **opts)
+
+    out_a, g_a, out_b, g_b = _both(fn, q, k, v, do)
+    assert torch.equal(out_a, out_b)
+    _check(g_a, g_b, dtype)
