@@ -228,9 +228,10 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
       const int64_t region = ds_region(p, b, hq, sq, sk);
       ds_on = region >= 0;
       S* const ws = reinterpret_cast<S*>(p.ds_workspace);
-      // row n % 64 of the key block's tiles; + (query block) * tile + m % 128
+      // row n % 64 of the key block's tiles; + (query block) * tile
+      //   + (query sub-tile) * sub-tile + q % 32
       dsn = ws + (ds_on ? region : 0) + (int64_t)(n / kDsTileKeys) * ds_qblocks(sq) * kDsTileElems +
-            (n % kDsTileKeys) * kDsTileQueries;
+            (n % kDsTileKeys) * kDsSubQueries;
       ds_dump = ws + (p.ds_workspace_bytes - 1024) / 2;
     }
     const VisBounds kvb = key_block_bounds(md, n0w, ncols);
@@ -372,8 +373,10 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
             w0[i] = r[0];
             w1[i] = r[1];
           }
+          static_assert(C::BMQ == kDsSubQueries, "a query step is one dS sub-tile");
           S* const at = !nvalid ? ds_dump
-                                : dsn + (int64_t)(m0 / kDsTileQueries) * kDsTileElems + (m0 % kDsTileQueries) + 16 * h;
+                                : dsn + (int64_t)(m0 / kDsTileQueries) * kDsTileElems +
+                                      (m0 % kDsTileQueries) / kDsSubQueries * kDsSubElems + 16 * h;
           // Nontemporal: the dS stream need not displace the Q / dO tiles
           // the other workgroups re-read from L2 (measured 3 us at config 2).
           __builtin_nontemporal_store(u32x4{w0[0], w0[1], w1[0], w1[1]}, reinterpret_cast<u32x4*>(at));
@@ -836,7 +839,7 @@ __global__ __launch_bounds__(512, 1) void dqs16_kernel(fa_bwd_params p, int num_
   DmaSwzTile<C::BN, D, C::NTH> kd;
   DmaSwzTile<C::BN, C::BM, C::NTH> sd;
   kd.init(ks, htid);
-  sd.init(C::BM, htid);
+  sd.template init_blocked<kDsSubQueries / 8>(kDsSubElems * 2, htid);
   const int nh0 = (ntiles + 1) / 2;
   const int my_first = khalf == 0 ? 0 : nh0;
   const int my_count = khalf == 0 ? nh0 : ntiles - nh0;
@@ -848,8 +851,12 @@ __global__ __launch_bounds__(512, 1) void dqs16_kernel(fa_bwd_params p, int num_
     const int rows = min(C::BN, sk - n0);
     const uint32_t base = lds0 + (uint32_t)(st * C::STAGE) * 2u;
     kd.load(rows_rsrc_words<D>(kbase + (int64_t)n0 * ks, ks, rows), base, wave);
-    const S* drows = dsbase + (int64_t)(n0 / kDsTileKeys) * qblocks * kDsTileElems + (n0 % kDsTileKeys) * C::BM;
-    sd.load(rows_rsrc_words<C::BM>(drows, C::BM, rows), base + C::KT * 2u, wave);
+    // The tile's 4 query sub-tiles hold rows of 32 queries; the window is
+    // the whole tile (rows past the last key are garbage there and are
+    // zeroed by the visibility mask of the partly visible step).
+    const int r0 = n0 % kDsTileKeys;  // first key row of the step within the tile
+    const S* dtile = dsbase + (int64_t)(n0 / kDsTileKeys) * qblocks * kDsTileElems + r0 * kDsSubQueries;
+    sd.load(rsrc_words(dtile, (kDsTileElems - r0 * kDsSubQueries) * 2), base + C::KT * 2u, wave);
   };
 
   // Visible keys of this lane's row: partly visible tiles zero the dS of

@@ -31,13 +31,17 @@ hipError_t launch_append(const fa_append_params& p, hipStream_t stream);
 size_t decode_workspace_bytes(int batch, int heads_q, int seqlen_q, int head_dim, int num_splits);
 
 // Score-gradient scratch of the 16-bit backward: per (sequence, query head)
-// a region of tiles of 64 keys x 128 queries (16 KiB of 16-bit dS, key-major
-// rows of 128 queries), tile (key block kb, query block qb) at
-// kb * ds_qblocks(Sq) + qb; the regions of a varlen batch are packed in
-// sequence order.  A dQ tile then reads 16 contiguous KiB.  The scratch ends
+// a region of tiles of 64 keys x 128 queries (16 KiB of 16-bit dS), tile
+// (key block kb, query block qb) at kb * ds_qblocks(Sq) + qb; the regions of
+// a varlen batch are packed in sequence order.  Inside a tile, queries come
+// in 4 sub-tiles of 32 (4 KiB each, key-major rows of 32 queries): element
+// (key n, query q) at (q / 32) * 2048 + n * 32 + q % 32.  A dK/dV step (32
+// queries) then writes whole 64-byte rows, 2 KiB contiguous per wave, and a
+// dQ step reads one tile's 16 contiguous KiB.  The scratch ends
 // in 1 KiB of slack where lanes past the last key of a dK/dV wave write.
 constexpr int kDsMaxVarlenBatch = 512;
 constexpr int kDsTileKeys = 64, kDsTileQueries = 128, kDsTileElems = kDsTileKeys * kDsTileQueries;
+constexpr int kDsSubQueries = 32, kDsSubElems = kDsTileKeys * kDsSubQueries;
 __host__ __device__ inline int64_t ds_qblocks(int sq) { return ((int64_t)sq + kDsTileQueries - 1) / kDsTileQueries; }
 __host__ __device__ inline int64_t ds_region_elems(int sq, int sk) {
   return ((int64_t)sk + kDsTileKeys - 1) / kDsTileKeys * ds_qblocks(sq) * kDsTileElems;

@@ -354,6 +354,19 @@ struct DmaSwzTile {
       voff[j] = (uint32_t)(row * stride * 2 + lc * 16);
     }
   }
+  // Source tile stored as column blocks of SUB_CHUNKS 16-byte chunks: row r
+  // of block k at k * block_bytes + r * SUB_CHUNKS * 16 (the LDS tile is the
+  // same row-major swizzled tile as with init).
+  template <int SUB_CHUNKS>
+  __device__ inline void init_blocked(int block_bytes, int tid) {
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      const int slot = NT * j + tid;
+      const int row = slot / CPR;
+      const int lc = (slot % CPR) ^ swz<COLS>(row);
+      voff[j] = (uint32_t)((lc / SUB_CHUNKS) * block_bytes + row * SUB_CHUNKS * 16 + (lc % SUB_CHUNKS) * 16);
+    }
+  }
   // lds_tile: byte address of the tile in LDS; wave: this wave's index.
   __device__ inline void load(i32x4 rs, uint32_t lds_tile, int wave) const {
 #pragma unroll
