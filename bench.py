@@ -153,6 +153,12 @@ def _flush(buf):
     buf.max()
 
 
+# Warm-up continues past the requested step count until this much wall time
+# of steps has run: the first ~0.1 s of back-to-back steps on a fresh box run
+# up to 20 % slower than the steady state (shader clock still ramping).
+MIN_WARMUP_S = 1.0
+
+
 def run_cfg2(steps, warmup):
     from fa_rdna3 import flash_attention
 
@@ -168,9 +174,14 @@ def run_cfg2(steps, warmup):
         out = flash_attention(q, k, v, causal=True, softmax_scale=scale)
         out.backward(do)
 
+    t_warm = time.perf_counter()
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    while time.perf_counter() - t_warm < MIN_WARMUP_S:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
@@ -522,6 +533,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_min_s": MIN_WARMUP_S,
         "ms_per_step": round(dt * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -18,6 +18,10 @@ DTYPE_CODE = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
 _LIB_NAME = "libfa_mi355x.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
+# PyTorch host glue of the dense forward / backward (csrc/fa_torch.cpp):
+# registers the torch.ops.fa_mi355x operators on top of the C ABI.
+_TORCH_LIB_NAME = "libfa_torch.so"
+_TORCH_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _TORCH_LIB_NAME)
 
 _i64_4 = ctypes.c_int64 * 4
 _i64_3 = ctypes.c_int64 * 3
@@ -174,8 +178,20 @@ def lib():
                 raise RuntimeError(
                     f"{struct.__name__} layout mismatch: library {handle.fa_params_size(which)} bytes, "
                     f"binding {ctypes.sizeof(struct)} bytes")
+        if not os.path.exists(_TORCH_LIB_PATH):
+            raise RuntimeError(
+                f"fa_rdna3 torch host library not found at {_TORCH_LIB_PATH}; build it with "
+                "`make -C flash-attention-rdna3_amd/csrc`")
+        torch.ops.load_library(_TORCH_LIB_PATH)
         _lib = handle
         return _lib
+
+
+def ops():
+    """The ``torch.ops.fa_mi355x`` namespace (dense forward / backward and
+    the differentiable ``attention``), loaded with the native library."""
+    lib()
+    return torch.ops.fa_mi355x
 
 
 def _check(rc, what):
@@ -202,9 +218,17 @@ def call_bwd_phase(params, phase, device_tensor):
     _check(lib().fa_bwd_phase(ctypes.byref(params), int(phase), _stream(device_tensor)), "fa_bwd_phase")
 
 
-# Largest score-gradient scratch the backward allocates; above it dQ
-# recomputes the scores instead of reading the stored dS.
-DS_SCRATCH_LIMIT_BYTES = 8 << 30
+def ds_scratch_limit():
+    """Largest score-gradient (dS) scratch a backward allocates, in bytes
+    (8 GiB by default); above it dQ recomputes the scores instead of
+    reading the stored dS.  0 means the dS path is off."""
+    return int(ops().ds_scratch_limit())
+
+
+def set_ds_scratch_limit(nbytes):
+    """Set the dS scratch limit for every backward of this process (dense and
+    varlen); returns the previous limit."""
+    return int(ops().set_ds_scratch_limit(int(nbytes)))
 
 
 def attach_ds_scratch(params, device_tensor):
@@ -212,7 +236,7 @@ def attach_ds_scratch(params, device_tensor):
     the single product dS K).  Returns the scratch tensor, which must stay
     alive until the launch is done, or None when the path does not apply."""
     need = int(lib().fa_bwd_workspace_bytes(ctypes.byref(params)))
-    if need == 0 or need > DS_SCRATCH_LIMIT_BYTES:
+    if need == 0 or need > ds_scratch_limit():
         params.ds_workspace, params.ds_workspace_bytes = None, 0
         return None
     buf = torch.empty(need, dtype=torch.uint8, device=device_tensor.device)

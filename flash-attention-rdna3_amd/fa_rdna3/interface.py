@@ -214,28 +214,19 @@ def _prep(*tensors):
 # ---------------------------------------------------------------------------
 
 def _forward(query, key, value, causal, softmax_scale, window, softcap, bias, alibi, dropout_p, dropout_seed):
-    batch, heads, seqlen_q, head_dim = query.shape
-    seqlen_k = key.shape[2]
-    kdim = _kernel_head_dim(head_dim)
-    q, k, v = _prep(_pad_head_dim(query, kdim), _pad_head_dim(key, kdim), _pad_head_dim(value, kdim))
-    out = torch.empty((batch, heads, seqlen_q, kdim), dtype=query.dtype, device=query.device)
-    lse = torch.empty((batch, heads, seqlen_q), dtype=torch.float32, device=query.device)
-    bias_t, *_, has_bias = _bias_args(bias, query, batch, heads, seqlen_q, seqlen_k)
-    alibi_t, has_alibi = _alibi_args(alibi, query)
-    params = _fwd_params(q, k, v, out, lse, dense=True, causal=causal, softmax_scale=softmax_scale,
-                         window=window, softcap=softcap, bias=bias_t if has_bias else None,
-                         alibi=alibi_t if has_alibi else None, dropout_p=dropout_p,
-                         dropout_seed=dropout_seed)
-    _native.call("fa_fwd", params, query)
-    if kdim != head_dim:
-        out = out[..., :head_dim].contiguous()
-    return out, lse
+    """Dense forward -> (out, lse) through the native host path
+    (``fa_mi355x::forward``: parameter packing and launch in C++)."""
+    return _native.ops().forward(query, key, value, bool(causal), float(softmax_scale), int(window[0]),
+                                 int(window[1]), float(softcap), bias, alibi, float(dropout_p),
+                                 int(dropout_seed))
 
 
 def _bwd_setup(dout, query, key, value, out, lse, causal, softmax_scale, window, softcap, bias, alibi,
                dropout_p, dropout_seed):
-    """Allocate dq/dk/dv/delta and fill fa_bwd_params for the dense backward.
-    Returns (params, dq, dk, dv, tensors kept alive for the launch)."""
+    """Allocate dq/dk/dv/delta and fill fa_bwd_params for one dense backward
+    phase at a time (``_backward_launcher``; the backward itself packs its
+    parameters in C++).  Returns (params, dq, dk, dv, tensors kept alive for
+    the launch)."""
     batch, heads, seqlen_q, head_dim = query.shape
     seqlen_k = key.shape[2]
     kdim = _kernel_head_dim(head_dim)
@@ -264,13 +255,11 @@ def _bwd_setup(dout, query, key, value, out, lse, causal, softmax_scale, window,
 
 def _backward(dout, query, key, value, out, lse, causal, softmax_scale, window, softcap, bias, alibi,
               dropout_p, dropout_seed):
-    head_dim = query.shape[-1]
-    params, dq, dk, dv, _keep = _bwd_setup(dout, query, key, value, out, lse, causal, softmax_scale,
-                                           window, softcap, bias, alibi, dropout_p, dropout_seed)
-    _native.call("fa_bwd", params, query)
-    if dq.shape[-1] != head_dim:
-        dq, dk, dv = dq[..., :head_dim], dk[..., :head_dim], dv[..., :head_dim]
-    return dq, dk, dv
+    """Dense backward -> (dq, dk, dv) through ``fa_mi355x::backward``
+    (delta, dK/dV and dQ in one C-ABI call, dS scratch when it fits)."""
+    return _native.ops().backward(dout, query, key, value, out, lse, bool(causal), float(softmax_scale),
+                                  int(window[0]), int(window[1]), float(softcap), bias, alibi,
+                                  float(dropout_p), int(dropout_seed))
 
 
 def _backward_launcher(dout, query, key, value, out, lse, causal, softmax_scale, window, softcap, bias,
@@ -340,30 +329,6 @@ def _flash_fwd_backward(ctx, grad_out, grad_lse):
 
 
 _flash_fwd.register_autograd(_flash_fwd_backward, setup_context=_flash_fwd_setup_context)
-
-
-class _FlashAttentionEager(torch.autograd.Function):
-    """Eager-mode twin of ``fa_rdna3::flash_fwd`` + its registered autograd:
-    same launches, without the custom-op dispatch layers (whose Python cost
-    per call is comparable to the kernels at training sizes).  Traced code
-    (torch.compile) goes through the op."""
-
-    @staticmethod
-    def forward(ctx, query, key, value, causal, softmax_scale, window_left, window_right,
-                softcap, bias, alibi, dropout_p, dropout_seed):
-        out, lse = _forward(query, key, value, causal, softmax_scale, (window_left, window_right),
-                            softcap, bias, alibi, dropout_p, dropout_seed)
-        ctx.save_for_backward(query, key, value, out, lse, bias, alibi)
-        ctx.args = (causal, softmax_scale, (window_left, window_right), softcap, dropout_p, dropout_seed)
-        return out
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        query, key, value, out, lse, bias, alibi = ctx.saved_tensors
-        causal, softmax_scale, window, softcap, dropout_p, dropout_seed = ctx.args
-        dq, dk, dv = _backward(grad_out.contiguous(), query, key, value, out, lse, causal, softmax_scale,
-                               window, softcap, bias, alibi, dropout_p, dropout_seed)
-        return dq, dk, dv, None, None, None, None, None, None, None, None, None
 
 
 # ---------------------------------------------------------------------------
@@ -472,8 +437,10 @@ def flash_attention(query, key, value, causal=False, softmax_scale=None, window_
         out, _ = _flash_fwd(query, key, value, causal, softmax_scale, window_size[0], window_size[1],
                             softcap, bias, alibi_slopes, dropout_p, dropout_seed)
     else:
-        out = _FlashAttentionEager.apply(query, key, value, causal, softmax_scale, window_size[0],
-                                         window_size[1], softcap, bias, alibi_slopes, dropout_p, dropout_seed)
+        # Eager mode: the differentiable native operator (forward launch, and
+        # a backward the autograd engine runs in C++ without Python).
+        out = _native.ops().attention(query, key, value, bool(causal), softmax_scale, int(window_size[0]),
+                                      int(window_size[1]), softcap, bias, alibi_slopes, dropout_p, dropout_seed)
     if pad:
         out = out[..., :head_dim]
     return out

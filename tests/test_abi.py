@@ -100,3 +100,18 @@ def test_bwd_ds_workspace_size():
     p.fwd.head_dim, p.fwd.dtype = 128, 2  # fp32
     assert lib.fa_bwd_workspace_bytes(ctypes.byref(p)) == 0
     assert lib.fa_bwd_workspace_bytes(None) == 0
+
+
+def test_torch_host_library_registers_its_operators():
+    """libfa_torch.so (the C++ host path of the dense forward / backward)
+    loads with the C-ABI library and registers its operators; the dS
+    scratch limit round-trips through it (no compute without a GPU)."""
+    ops = _native.ops()
+    for name in ("attention", "forward", "backward", "set_ds_scratch_limit", "ds_scratch_limit"):
+        assert hasattr(ops, name), name
+    saved = _native.set_ds_scratch_limit(12345)
+    try:
+        assert _native.ds_scratch_limit() == 12345
+    finally:
+        _native.set_ds_scratch_limit(saved)
+    assert _native.ds_scratch_limit() == saved

@@ -24,12 +24,11 @@ def _both(fn, *tensors):
         return out.detach(), [t.grad for t in leaves]
 
     out_a, g_a = run()
-    saved = _native.DS_SCRATCH_LIMIT_BYTES
-    _native.DS_SCRATCH_LIMIT_BYTES = 0
+    saved = _native.set_ds_scratch_limit(0)
     try:
         out_b, g_b = run()
     finally:
-        _native.DS_SCRATCH_LIMIT_BYTES = saved
+        _native.set_ds_scratch_limit(saved)
     return out_a, g_a, out_b, g_b
 
 
