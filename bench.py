@@ -383,9 +383,12 @@ def run_cfg5(iters=5):
         out = flash_attention_varlen(q, k, v, cu, cu, mx, mx, causal=True, window_size=(1024, -1), softcap=50.0)
         out.backward(do)
 
-    for _ in range(2):
-        step()
+    t_warm = time.perf_counter()
+    step()
     torch.cuda.synchronize()
+    while time.perf_counter() - t_warm < MIN_WARMUP_S:
+        step()
+        torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(iters):
         step()

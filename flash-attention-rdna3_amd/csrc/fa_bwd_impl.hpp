@@ -566,6 +566,16 @@ static hipError_t run_bwd_dkdv16(const fa_bwd_params& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <typename Tag, int D, int OCC>
+static hipError_t launch_dqs16(const fa_bwd_params& p, long grid, int nmb, float dq_scale, hipStream_t stream) {
+  using C = Dqs16Cfg<D, OCC>;
+  auto kern = dqs16_kernel<Tag, D, OCC>;
+  hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb, dq_scale);
+  return hipGetLastError();
+}
+
 template <typename Tag, int D, int MODE>
 static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream) {
   const fa_fwd_params& f = p.fwd;
@@ -600,16 +610,19 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
         if (e != hipSuccess) return e;
         phases &= ~2;
       }
-      using C = Dqs16Cfg<D>;
-      auto kern = dqs16_kernel<Tag, D>;
-      hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
-      if (e != hipSuccess) return e;
-      const int nmb = (f.seqlen_q + C::BM - 1) / C::BM;
+      const int nmb = (f.seqlen_q + Dqs16Cfg<D, 1>::BM - 1) / Dqs16Cfg<D, 1>::BM;
       const long grid = (long)nmb * f.batch * f.heads_q;
       // MODE 3 stores dS / 4 (its softcap factor is (1 - tanh^2) / 4).
       const float dq_scale = f.softmax_scale * (MODE == 3 ? 4.f : 1.f);
-      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb, dq_scale);
-      e = hipGetLastError();
+      // Two workgroups per CU (D = 128) once the launch spans more than
+      // three rounds of one workgroup per CU.
+      hipError_t e;
+      if constexpr (D >= 128) {
+        e = grid > 3L * device_cu_count() ? launch_dqs16<Tag, D, 2>(p, grid, nmb, dq_scale, stream)
+                                          : launch_dqs16<Tag, D, 1>(p, grid, nmb, dq_scale, stream);
+      } else {
+        e = launch_dqs16<Tag, D, 1>(p, grid, nmb, dq_scale, stream);
+      }
       if (e != hipSuccess) return e;
     }
     }

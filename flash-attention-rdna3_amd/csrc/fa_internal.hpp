@@ -51,4 +51,7 @@ size_t bwd_ds_bytes(const fa_bwd_params& p);
 // Raise a kernel's dynamic LDS limit once per process (gfx950: 160 KiB/CU).
 hipError_t allow_lds(const void* kernel, int bytes);
 
+// Compute units of the current device (cached per device).
+int device_cu_count();
+
 }  // namespace fa
