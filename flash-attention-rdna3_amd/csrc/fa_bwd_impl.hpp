@@ -34,37 +34,67 @@ namespace fa {
 // ---------------------------------------------------------------------------
 // delta[m] = sum_d O[m][d] * dO[m][d]   (fp32 accumulate)
 // ---------------------------------------------------------------------------
+// Rows per thread of the delta pass: four 16-byte chunks of O and of dO in
+// flight per thread (one row of D = 512 f16, four rows of D = 128 f16).
+template <typename Tag, int D>
+constexpr int delta_rows_per_thread() {
+  constexpr int chunks = (D / Elem<Tag>::CE + 15) / 16;
+  return chunks >= 4 ? 1 : 4 / chunks;
+}
+
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void bwd_delta_kernel(fa_bwd_params p) {
   using EL = Elem<Tag>;
   using S = typename EL::S;
   constexpr int CE = EL::CE, CPR = D / CE;
   constexpr int LPR = 16;  // lanes per row
+  // Each thread covers R rows 16 apart and issues all of their loads before
+  // the products, so a wave keeps R times more bytes in flight than a
+  // one-row pass.
+  constexpr int R = delta_rows_per_thread<Tag, D>();
   const fa_fwd_params& f = p.fwd;
   const int bh = blockIdx.y, b = bh / f.heads_q, hq = bh - b * f.heads_q;
   int q_start = 0, sq = f.seqlen_q;
   if (f.cu_seqlens_q) bounded_seq(f.cu_seqlens_q, b, f.total_q, q_start, sq);
-  const int m = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int mrow = blockIdx.x * (16 * R) + (threadIdx.x >> 4);
+  if (blockIdx.x * (16 * R) >= sq) return;
   const int sub = threadIdx.x & 15;
-  float acc = 0.f;
-  if (m < sq) {
-    const S* o = reinterpret_cast<const S*>(f.out) + b * f.out_stride[0] + hq * f.out_stride[1] +
-                 (int64_t)(q_start + m) * f.out_stride[2];
-    const S* g = reinterpret_cast<const S*>(p.dout) + b * p.dout_stride[0] + hq * p.dout_stride[1] +
-                 (int64_t)(q_start + m) * p.dout_stride[2];
-    for (int c = sub; c < CPR; c += LPR) {
-      uint4 a = *reinterpret_cast<const uint4*>(o + c * CE);
-      uint4 bb = *reinterpret_cast<const uint4*>(g + c * CE);
-      const S* av = reinterpret_cast<const S*>(&a);
-      const S* bv = reinterpret_cast<const S*>(&bb);
+  const S* obase = reinterpret_cast<const S*>(f.out) + b * f.out_stride[0] + hq * f.out_stride[1];
+  const S* gbase = reinterpret_cast<const S*>(p.dout) + b * p.dout_stride[0] + hq * p.dout_stride[1];
+  constexpr int NC = (CPR + LPR - 1) / LPR;  // chunks per lane per row
+  uint4 a[R][NC], g[R][NC];
 #pragma unroll
-      for (int e = 0; e < CE; ++e) acc += EL::to_f(av[e]) * EL::to_f(bv[e]);
+  for (int r = 0; r < R; ++r) {
+    const int m = min(mrow + 16 * r, sq - 1);
+    const S* o = obase + (int64_t)(q_start + m) * f.out_stride[2];
+    const S* d = gbase + (int64_t)(q_start + m) * p.dout_stride[2];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = sub + i * LPR;
+      if (c < CPR) {
+        a[r][i] = *reinterpret_cast<const uint4*>(o + c * CE);
+        g[r][i] = *reinterpret_cast<const uint4*>(d + c * CE);
+      }
     }
   }
 #pragma unroll
-  for (int w = 8; w >= 1; w >>= 1) acc += __shfl_xor(acc, w, 64);
-  if (m < sq && sub == 0)
-    p.delta[b * p.delta_stride[0] + hq * p.delta_stride[1] + (int64_t)(q_start + m) * p.delta_stride[2]] = acc;
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      if (sub + i * LPR < CPR) {
+        const S* av = reinterpret_cast<const S*>(&a[r][i]);
+        const S* bv = reinterpret_cast<const S*>(&g[r][i]);
+#pragma unroll
+        for (int e = 0; e < CE; ++e) acc += EL::to_f(av[e]) * EL::to_f(bv[e]);
+      }
+    }
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1) acc += __shfl_xor(acc, w, 64);
+    const int m = mrow + 16 * r;
+    if (m < sq && sub == 0)
+      p.delta[b * p.delta_stride[0] + hq * p.delta_stride[1] + (int64_t)(q_start + m) * p.delta_stride[2]] = acc;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -595,7 +625,8 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
   }
   const bool fused_delta = fast_ok && !use_ds && (phases & 1) && (phases & 4);
   if ((phases & 1) && !fused_delta) {
-    dim3 grid((f.seqlen_q + 15) / 16, f.batch * f.heads_q);
+    constexpr int rows = 16 * delta_rows_per_thread<Tag, D>();
+    dim3 grid((f.seqlen_q + rows - 1) / rows, f.batch * f.heads_q);
     hipLaunchKernelGGL((bwd_delta_kernel<Tag, D>), grid, dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
