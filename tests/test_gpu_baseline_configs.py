@@ -83,6 +83,7 @@ def test_cfg5_varlen_window_softcap():
         s, n = starts[i], lengths[i]
         ref = varlen_attention(q[s:s + n].float(), k[s:s + n].float(), v[s:s + n].float(), [n], [n], **kw)
         err = max_err(out[s:s + n], ref)
+        print(f"cfg5 seq {i} ({n}) out: err {err:.3e}", flush=True)
         assert err <= 1e-2, (i, n, err)
     # Gradients: sequences 14 and 0 (2023 and 1937 tokens) are longer than the
     # 1024-key window, so the window bites; 13 and 3 are shorter than it.
