@@ -202,7 +202,7 @@ def gemm_ceiling(n=8192, iters=10):
     return 2.0 * n ** 3 / (ms * 1e-3) / 1e12
 
 
-def dkdv_roofline(tensors, iters=50):
+def dkdv_roofline(tensors, iters=100):
     """Time the dK/dV kernel alone (fa_bwd phase 1) with HIP events."""
     from fa_rdna3 import interface as I
 
@@ -224,7 +224,7 @@ def dkdv_roofline(tensors, iters=50):
             "traffic": DKDV_TRAFFIC_BYTES, "avg_us": round(ms * 1e3, 2), "flops_per_launch": flops}
 
 
-def run_decode_configs(iters=50):
+def run_decode_configs(iters=100):
     from fa_rdna3 import (flash_attention_decode, flash_attention_decode_paged, flash_attention_decode_paged_multi,
                           flash_attention_with_kvcache)
 
@@ -369,7 +369,7 @@ def run_decode_configs(iters=50):
     return res
 
 
-def run_cfg5(iters=5):
+def run_cfg5(iters=20):
     from fa_rdna3 import flash_attention_varlen
 
     lengths, q, k, v, do, cu = workload_cfg5()
@@ -500,7 +500,7 @@ def pmc_summary(dirs):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip decode/varlen side measurements")
