@@ -31,10 +31,18 @@ namespace fa {
 // LDS at the end.  One 8-wave workgroup fills a CU at two waves per SIMD, so
 // a heavy causal block runs at full CU throughput instead of sharing the CU
 // with a light one and then running alone.
-template <int D>
+//
+// NH = 1 is the same kernel with one key half: 4 waves walk all key tiles of
+// the 128 rows and no merge is needed.  Its 64 KiB of LDS and 4 waves let two
+// workgroups share a CU, so one workgroup's prologue (Q and first tiles) and
+// epilogue (output store) overlap the other's steady state.  It is launched
+// when the grid spans many rounds of workgroups (a packed varlen batch),
+// where that per-workgroup cost adds up; a short causal batch keeps NH = 2,
+// whose key split lets a heavy block use the whole CU.
+template <int D, int NH = 2>
 struct Fwd16Cfg {
   static constexpr int NQ = 4;                 // row quarters (waves per half)
-  static constexpr int NW = 2 * NQ;
+  static constexpr int NW = NH * NQ;
   static constexpr int NT = 64 * NW;
   static constexpr int NTH = 64 * NQ;          // threads per key half
   static constexpr int BM = 32 * NQ;
@@ -42,8 +50,8 @@ struct Fwd16Cfg {
   static constexpr int KTILE = BN * D;  // elements (K), then V
   static constexpr int STAGE = 2 * KTILE;
   static constexpr int HALF = 2 * STAGE;       // two stages per key half
-  static constexpr int MERGE_BYTES = NQ * (D / 32) * 16 * 64 * 4 + 2 * NQ * 64 * 4;
-  static constexpr int LOOP_BYTES = 2 * HALF * 2;
+  static constexpr int MERGE_BYTES = NH == 1 ? 0 : NQ * (D / 32) * 16 * 64 * 4 + 2 * NQ * 64 * 4;
+  static constexpr int LOOP_BYTES = NH * HALF * 2;
   static constexpr int LDS_BYTES = LOOP_BYTES > MERGE_BYTES ? LOOP_BYTES : MERGE_BYTES;
   static constexpr int NSTEP = D / 16;
   static constexpr int NKB = BN / 32;
@@ -54,9 +62,9 @@ struct Fwd16Cfg {
 // Largest growth of the running max (log2 domain) absorbed without rescaling.
 constexpr float kLazyRescale = 8.0f;
 
-template <typename Tag, int D, int MODE>
-__global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_m_blocks) {
-  using C = Fwd16Cfg<D>;
+template <typename Tag, int D, int MODE, int NH>
+__global__ __launch_bounds__(256 * NH, 3 - NH) void fwd16_kernel(fa_fwd_params p, int num_m_blocks) {
+  using C = Fwd16Cfg<D, NH>;
   using EL = Elem<Tag>;
   using S = uint16_t;
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -118,13 +126,13 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
   kt.init(ks, htid);
   vt.init(vs, htid);
   // Both halves run nh0 steps so their barriers line up.
-  const int nh0 = (ntiles + 1) / 2;
+  const int nh0 = NH == 1 ? ntiles : (ntiles + 1) / 2;
   // Half 0 takes the even key tiles, half 1 the odd ones: the two masked
   // diagonal tiles of a causal block then fall into the same step instead of
   // two steps in which half 0 waits for half 1.
   const int my_first = khalf;
-  constexpr int TSTEP = 2;
-  const int my_count = khalf == 0 ? nh0 : ntiles - nh0;
+  constexpr int TSTEP = NH;
+  const int my_count = NH == 1 ? ntiles : khalf == 0 ? nh0 : ntiles - nh0;
   const uint32_t lds0 = lds_addr(smem) + (uint32_t)(khalf * C::HALF) * 2u;
   // Tile sources advance by BN rows per load (scalar pointer arithmetic).
   int n_next = lo + my_first * C::BN;
@@ -322,7 +330,7 @@ __global__ __launch_bounds__(512, 1) void fwd16_kernel(fa_fwd_params p, int num_
 
   // Merge the two key halves: half 1 parks (O^T, m, l) in LDS, half 0 folds
   // them into its own state.  Both are relative to their own running max.
-  {
+  if constexpr (NH == 2) {
     float* ow = reinterpret_cast<float*>(smem_raw);
     float* mw = ow + C::NQ * C::NDB * 16 * 64;
     float* lw = mw + C::NQ * 64;

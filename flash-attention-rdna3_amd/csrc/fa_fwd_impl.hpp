@@ -273,19 +273,32 @@ __global__ __launch_bounds__(256) void fwd_kernel(fa_fwd_params p, int num_m_blo
     lb[(int64_t)m * p.lse_stride[2]] = (m_i == kNegInf) ? kNegInf : (m_i + __log2f(l_safe)) * kLn2;
 }
 
+template <typename Tag, int D, int MODE, int NH>
+static hipError_t launch_fwd16(const fa_fwd_params& p, long grid, int nmb, hipStream_t stream) {
+  using C = Fwd16Cfg<D, NH>;
+  auto kern = fwd16_kernel<Tag, D, MODE, NH>;
+  hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb);
+  return hipGetLastError();
+}
+
 template <typename Tag, int D, int MODE>
 static hipError_t run_fwd(const fa_fwd_params& p, hipStream_t stream) {
   if constexpr (!std::is_same<Tag, f32_t>::value && D <= 128) {
     using C = Fwd16Cfg<D>;
     if (buf_rows_ok(p.k_stride[2], C::BN) && buf_rows_ok(p.v_stride[2], C::BN)) {
-    auto kern = fwd16_kernel<Tag, D, MODE>;
-    hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
-    if (e != hipSuccess) return e;
     const int nmb = (p.seqlen_q + C::BM - 1) / C::BM;
     const long grid = (long)nmb * p.batch * p.heads_q;
     if (grid <= 0) return hipSuccess;
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb);
-    return hipGetLastError();
+    // One key half, two workgroups per CU, for packed varlen batches and for
+    // dense grids of more than eight rounds of one 8-wave workgroup per CU.
+    // (Varlen always: a sequence's output then does not depend on the batch
+    // it is packed with.  The two forms sum the key tiles in different
+    // orders, so they agree to rounding, not bit for bit.)
+    if (p.cu_seqlens_q || grid > 8L * device_cu_count())
+      return launch_fwd16<Tag, D, MODE, 1>(p, grid, nmb, stream);
+    return launch_fwd16<Tag, D, MODE, 2>(p, grid, nmb, stream);
     }
   }
   // The generic kernel has no softcap-only variant (MODE 3 is MODE 1 there).

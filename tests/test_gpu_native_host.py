@@ -91,3 +91,21 @@ def test_backward_follows_the_ds_scratch_limit():
     for x, y in zip(a[:2], b[:2]):
         scale = y.float().abs().max().item()
         assert (x.float() - y.float()).abs().max().item() <= 4 * 2 ** -10 * max(scale, 1e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_forward_configurations_agree(dtype):
+    """A dense grid of many workgroups runs the one-key-half forward (two
+    workgroups per CU), a small one the key-split forward: the same rows
+    through both agree to the output rounding, and the LSE to 1e-5."""
+    # 4 row blocks x 640 (batch, head): 2560 workgroups, above 8 per CU of
+    # the 256-CU MI355X, so the one-half form runs
+    big = tuple(_rand((40, 16, 512, 128), dtype, s) for s in (1, 2, 3))
+    out_b, lse_b = _forward(*big, True, 128 ** -0.5, (-1, -1), 0.0, None, None, 0.0, 0)
+    one = tuple(t[:1].contiguous() for t in big)  # 64 blocks: key-split form
+    out_1, lse_1 = _forward(*one, True, 128 ** -0.5, (-1, -1), 0.0, None, None, 0.0, 0)
+    ulp = 2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7
+    bound = 2 * ulp * out_1.float().abs().clamp_min(1.0)
+    assert torch.all((out_b[:1].float() - out_1.float()).abs() <= bound)
+    assert not torch.equal(out_b[:1], out_1)  # the two forms did run
+    assert (lse_b[:1] - lse_1).abs().max().item() <= 1e-5
