@@ -310,7 +310,11 @@ struct BufSwzTile {
 // slot is its own, so the tile lands in the swz<COLS> layout.  The load is
 // issued from inline asm: the compiler does not track it, so it neither
 // drains it before unrelated LDS reads nor waits for it at all -- the kernel
-// waits (vmcnt) and synchronises (barrier) before reading the tile.
+// waits (vmcnt) and synchronises (barrier) before reading the tile.  The asm
+// writes M0, which the compiler reserves (hence its -Winline-asm warning):
+// no other instruction of these kernels reads M0 (no LDS-direct, movrel,
+// GWS or message instructions; the generated code was checked), so nothing
+// depends on a value the asm overwrites.
 // ---------------------------------------------------------------------------
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
