@@ -414,26 +414,17 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
     }
   }
 
-  if (!nvalid) return;
-  S* dkr = reinterpret_cast<S*>(p.dk) + b * p.dk_stride[0] + hk * p.dk_stride[1] +
-           (int64_t)(k_start + n) * p.dk_stride[2];
-  S* dvr = reinterpret_cast<S*>(p.dv) + b * p.dv_stride[0] + hk * p.dv_stride[1] +
-           (int64_t)(k_start + n) * p.dv_stride[2];
+  // Whole-row dK / dV stores through this wave's two LDS blocks of the
+  // merge above (read back already).
+  S* dkr0 = reinterpret_cast<S*>(p.dk) + b * p.dk_stride[0] + hk * p.dk_stride[1] +
+            (int64_t)(k_start + n0w) * p.dk_stride[2];
+  S* dvr0 = reinterpret_cast<S*>(p.dv) + b * p.dv_stride[0] + hk * p.dv_stride[1] +
+            (int64_t)(k_start + n0w) * p.dv_stride[2];
   const float sc = f.softmax_scale * (MODE == 3 ? 4.f : 1.f);
-#pragma unroll
-  for (int db = 0; db < C::NDB; ++db)
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const int d = db * 32 + 8 * gq + 4 * h;
-      s16x4 wk, wv;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        wk[r] = (short)EL::from_f(dk[db][4 * gq + r] * sc);
-        wv[r] = (short)EL::from_f(dv[db][4 * gq + r]);
-      }
-      *reinterpret_cast<s16x4*>(dkr + d) = wk;
-      *reinterpret_cast<s16x4*>(dvr + d) = wv;
-    }
+  unsigned char* const wblk = smem_raw + wave * 2 * C::NDB * 4096;
+  store_rows_staged<Tag, D>(dk, sc, reinterpret_cast<uint16_t*>(wblk), dkr0, p.dk_stride[2], ncols, lane);
+  store_rows_staged<Tag, D>(dv, 1.f, reinterpret_cast<uint16_t*>(wblk + C::NDB * 4096), dvr0, p.dv_stride[2],
+                            ncols, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -932,18 +923,11 @@ __global__ __launch_bounds__(512, OCC) void dqs16_kernel(fa_bwd_params p, int nu
     for (int db = 0; db < C::NDB; ++db) dq[db] += unpark_acc(ow + (wave * C::NDB + db) * 1024, lane);
   }
 
-  if (!mvalid) return;
-  S* dqr = reinterpret_cast<S*>(p.dq) + b * p.dq_stride[0] + hq * p.dq_stride[1] +
-           (int64_t)(q_start + m) * p.dq_stride[2];
-#pragma unroll
-  for (int db = 0; db < C::NDB; ++db)
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      s16x4 w;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) w[r] = (short)EL::from_f(dq[db][4 * gq + r] * dq_scale);
-      *reinterpret_cast<s16x4*>(dqr + db * 32 + 8 * gq + 4 * h) = w;
-    }
+  // Whole-row dQ stores through this wave's LDS block of the merge above.
+  S* dqr0 = reinterpret_cast<S*>(p.dq) + b * p.dq_stride[0] + hq * p.dq_stride[1] +
+            (int64_t)(q_start + m0w) * p.dq_stride[2];
+  store_rows_staged<Tag, D>(dq, dq_scale, reinterpret_cast<uint16_t*>(smem_raw + wave * C::NDB * 4096), dqr0,
+                            p.dq_stride[2], mrows, lane);
 }
 
 }  // namespace fa

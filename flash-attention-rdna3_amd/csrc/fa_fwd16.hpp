@@ -356,20 +356,16 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void fwd16_kernel(fa_fwd_params p
     m_i = mn;
   }
 
-  if (!mvalid) return;
   const float l_safe = (l_i == 0.f) ? 1.f : l_i;
   const float inv = 1.f / l_safe;
-  S* orow = reinterpret_cast<S*>(p.out) + b * p.out_stride[0] + hq * p.out_stride[1] +
-            (int64_t)(q_start + m) * p.out_stride[2];
-#pragma unroll
-  for (int db = 0; db < C::NDB; ++db)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      s16x4 w;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) w[r] = (short)EL::from_f(acc[db][4 * g + r] * inv);
-      *reinterpret_cast<s16x4*>(orow + db * 32 + 8 * g + 4 * h) = w;
-    }
+  // Whole-row output stores through this wave's LDS block: with NH = 2 the
+  // block this wave's merge partner parked into (read above), with NH = 1 a
+  // stage buffer (every tile read ended at the loop's last barrier).
+  S* orow0 = reinterpret_cast<S*>(p.out) + b * p.out_stride[0] + hq * p.out_stride[1] +
+             (int64_t)(q_start + m0w) * p.out_stride[2];
+  store_rows_staged<Tag, D>(acc, inv, reinterpret_cast<uint16_t*>(smem_raw + wave * C::NDB * 4096), orow0,
+                            p.out_stride[2], mrows, lane);
+  if (!mvalid) return;
   if (h == 0) {
     float* lb = p.lse + b * p.lse_stride[0] + hq * p.lse_stride[1] + (int64_t)(q_start + m) * p.lse_stride[2];
     *lb = (m_i == kNegInf || l_i == 0.f) ? kNegInf : (m_i + __log2f(l_safe)) * kLn2;

@@ -431,4 +431,43 @@ __device__ inline f32x16 unpark_acc(const float* blk, int lane) {
   return a;
 }
 
+// Whole-row store of a wave's 32 x D 16-bit output held as 32x32 MFMA
+// accumulators (lane%32 = row, acc[db][4g + r] = column 32 db + 8 g + 4 h + r,
+// h = lane/32).  Written straight from that layout, every store instruction
+// would put 8 bytes into each of 32 rows, i.e. partial 128-byte lines in
+// HBM (twice the output bytes were written back).  Instead the rows go
+// through LDS (kStageRowBytes per row, padded so the 32 lanes' writes of
+// one column fall in distinct banks), then each lane stores 16 consecutive
+// bytes and a wave instruction covers 64 x 16 bytes of whole rows.
+// `stage` is this wave's LDS area of 32 * (D + 8) halfs (8.5 KiB at
+// D = 128), not used by any other wave at this point; all 64 lanes must
+// call (rows >= nrows are staged but not stored).
+template <typename Tag, int D>
+__device__ inline void store_rows_staged(const f32x16 (&acc)[D / 32], float scale, uint16_t* stage,
+                                         uint16_t* out_row0, int64_t row_stride, int nrows, int lane) {
+  using EL = Elem<Tag>;
+  constexpr int RS = D + 8;  // staged row stride (halfs): 16-byte aligned rows
+  const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      s16x4 w;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[r] = (short)EL::from_f(acc[db][4 * g + r] * scale);
+      *reinterpret_cast<s16x4*>(stage + l32 * RS + db * 32 + 8 * g + 4 * h) = w;
+    }
+  // (a wave's LDS operations complete in issue order: the reads below see
+  // every lane's writes above)
+  constexpr int CPR = D / 8;       // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;    // rows per wave instruction
+  const int rsub = lane / CPR, ch = lane % CPR;
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int row = i * RPI + rsub;
+    const s16x8 v = *reinterpret_cast<const s16x8*>(stage + row * RS + ch * 8);
+    if (row < nrows) *reinterpret_cast<s16x8*>(out_row0 + (int64_t)row * row_stride + ch * 8) = v;
+  }
+}
+
 }  // namespace fa
