@@ -109,3 +109,49 @@ def test_forward_configurations_agree(dtype):
     assert torch.all((out_b[:1].float() - out_1.float()).abs() <= bound)
     assert not torch.equal(out_b[:1], out_1)  # the two forms did run
     assert (lse_b[:1] - lse_1).abs().max().item() <= 1e-5
+
+
+@pytest.mark.parametrize("mods", [dict(window=(200, 0)), dict(softcap=30.0), dict(alibi=True), dict(bias=True)],
+                         ids=["window", "softcap", "alibi", "bias"])
+def test_forward_configurations_agree_with_modifiers(mods):
+    """The one-key-half forward (large grid) against the key-split forward
+    (small grid) on the same rows, with each score modifier."""
+    dt = torch.bfloat16
+    big = tuple(_rand((40, 16, 512, 128), dt, s) for s in (5, 6, 7))
+    h = 16
+    bias = _rand((1, h, 512, 512), torch.float32, 8) if mods.get("bias") else None
+    alibi = alibi_slopes(h) if mods.get("alibi") else None
+    args = (True, 128 ** -0.5, mods.get("window", (-1, -1)), mods.get("softcap", 0.0), bias, alibi, 0.0, 0)
+    out_b, lse_b = _forward(*big, *args)
+    out_1, lse_1 = _forward(*(t[:1].contiguous() for t in big), *args)
+    bound = 2 * 2.0 ** -7 * out_1.float().abs().clamp_min(1.0)
+    assert torch.all((out_b[:1].float() - out_1.float()).abs() <= bound)
+    fin = torch.isfinite(lse_1)
+    assert torch.equal(fin, torch.isfinite(lse_b[:1]))
+    assert (lse_b[:1][fin] - lse_1[fin]).abs().max().item() <= 1e-5
+
+
+def test_two_per_cu_dq_form_on_a_dense_grid():
+    """A dense causal grid above three rounds of workgroups per CU runs dQ
+    from stored dS in its two-per-CU form (16-key steps); its dQ equals,
+    bit for bit, the one-per-CU form's on the same sequence (same products
+    in the same order), and agrees with the recomputing dQ."""
+    dt = torch.float16
+    q, k, v, do = (_rand((8, 16, 1024, 128), dt, s) for s in (11, 12, 13, 14))  # 8 x 128 = 1024 workgroups
+
+    def dq(*t):
+        leaves = [x.detach().clone().requires_grad_(True) for x in t[:3]]
+        flash_attention(*leaves, causal=True).backward(t[3])
+        return [x.grad for x in leaves]
+
+    big = dq(q, k, v, do)
+    one = dq(*(t[:1].contiguous() for t in (q, k, v, do)))  # 128 workgroups: one-per-CU form
+    for a, b in zip(big, one):
+        assert torch.equal(a[:1], b)
+    saved = _native.set_ds_scratch_limit(0)
+    try:
+        rec = dq(q, k, v, do)
+    finally:
+        _native.set_ds_scratch_limit(saved)
+    scale = rec[0].float().abs().max().item()
+    assert (big[0].float() - rec[0].float()).abs().max().item() <= 4 * 2 ** -10 * max(scale, 1e-3)
