@@ -29,6 +29,7 @@
 
 #include <atomic>
 #include <cstring>
+#include <initializer_list>
 #include <optional>
 #include <tuple>
 
@@ -152,9 +153,22 @@ Extras fill_fwd(fa_fwd_params& p, const Tensor& q, const Tensor& k, const Tensor
   return ex;
 }
 
+// Every tensor a launch touches must live on the query's GPU: the C ABI
+// receives bare pointers and cannot tell host memory from device memory.
+void check_on_gpu(const Tensor& query, std::initializer_list<const Tensor*> others, const Options& o) {
+  TORCH_CHECK(query.is_cuda(), "fa_mi355x: tensors must be on a GPU");
+  for (const Tensor* t : others)
+    TORCH_CHECK(t->device() == query.device(), "fa_mi355x: all tensors must be on the query's device");
+  if (o.bias.has_value() && o.bias->defined())
+    TORCH_CHECK(o.bias->device() == query.device(), "fa_mi355x: bias must be on the query's device");
+  if (o.alibi.has_value() && o.alibi->defined())
+    TORCH_CHECK(o.alibi->device() == query.device(), "fa_mi355x: alibi slopes must be on the query's device");
+}
+
 // reference interface.py:154-199 (_forward)
 std::tuple<Tensor, Tensor> forward_impl(const Tensor& query, const Tensor& key, const Tensor& value,
                                         const Options& o) {
+  check_on_gpu(query, {&key, &value}, o);
   c10::DeviceGuard guard(query.device());
   const int64_t head_dim = query.size(3);
   const int64_t kdim = std::max(kMinKernelHeadDim, head_dim);
@@ -175,6 +189,7 @@ std::tuple<Tensor, Tensor> forward_impl(const Tensor& query, const Tensor& key, 
 std::tuple<Tensor, Tensor, Tensor> backward_impl(const Tensor& dout, const Tensor& query, const Tensor& key,
                                                  const Tensor& value, const Tensor& out, const Tensor& lse_in,
                                                  const Options& o) {
+  check_on_gpu(query, {&dout, &key, &value, &out, &lse_in}, o);
   c10::DeviceGuard guard(query.device());
   const int64_t head_dim = query.size(3);
   const int64_t kdim = std::max(kMinKernelHeadDim, head_dim);

@@ -115,3 +115,18 @@ def test_torch_host_library_registers_its_operators():
     finally:
         _native.set_ds_scratch_limit(saved)
     assert _native.ds_scratch_limit() == saved
+
+
+def test_torch_host_operators_refuse_host_tensors():
+    """The native operators hand bare pointers to the C ABI, so they refuse
+    tensors that are not on a GPU before any launch (no GPU needed)."""
+    import torch
+
+    ops = _native.ops()
+    q = torch.zeros(1, 1, 8, 64, dtype=torch.float16)
+    args = (True, 0.125, -1, -1, 0.0, None, None, 0.0, 0)
+    for fn in (ops.attention, ops.forward):
+        with pytest.raises(Exception, match="GPU|CUDA|backend"):
+            fn(q, q, q, *args)
+    with pytest.raises(Exception, match="GPU|CUDA|backend"):
+        ops.backward(q, q, q, q, q, torch.zeros(1, 1, 8), *args)
