@@ -62,12 +62,16 @@ struct Fwd16Cfg {
 // Largest growth of the running max (log2 domain) absorbed without rescaling.
 constexpr float kLazyRescale = 8.0f;
 
+// One work item: the 128 query rows of row block (num_m_blocks - 1 - mb_rev)
+// of (batch, head) bh, item = mb_rev * B * Hq + bh.  `end_barrier`: the
+// workgroup runs another item after this one, so every wave passes a
+// barrier once this item's LDS use (merge, staged stores) is over.
 template <typename Tag, int D, int MODE, int NH>
-__global__ __launch_bounds__(256 * NH, 3 - NH) void fwd16_kernel(fa_fwd_params p, int num_m_blocks) {
+__device__ __forceinline__ void fwd16_item(const fa_fwd_params& p, int num_m_blocks, int item,
+                                           unsigned char* smem_raw, bool end_barrier) {
   using C = Fwd16Cfg<D, NH>;
   using EL = Elem<Tag>;
   using S = uint16_t;
-  extern __shared__ __align__(16) unsigned char smem_raw[];
   S* smem = reinterpret_cast<S*>(smem_raw);
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -78,8 +82,8 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void fwd16_kernel(fa_fwd_params p
   const int h = lane >> 5, l32 = lane & 31;
 
   const int bh_count = p.batch * p.heads_q;
-  const int mb_rev = blockIdx.x / bh_count;
-  const int bh = blockIdx.x - mb_rev * bh_count;
+  const int mb_rev = item / bh_count;
+  const int bh = item - mb_rev * bh_count;
   const int b = bh / p.heads_q, hq = bh - b * p.heads_q;
   const int hk = hq / (p.heads_q / p.heads_kv);
   const int mblk = num_m_blocks - 1 - mb_rev;  // heaviest causal blocks first
@@ -341,7 +345,10 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void fwd16_kernel(fa_fwd_params p
       lw[wave * 64 + lane] = l_i;
     }
     __syncthreads();
-    if (khalf == 1) return;
+    if (khalf == 1) {
+      if (end_barrier) __syncthreads();
+      return;
+    }
     const float mb2 = mw[wave * 64 + lane], lb2 = lw[wave * 64 + lane];
     const float mn = fmaxf(m_i, mb2);
     const float mu = (mn == kNegInf) ? 0.f : mn;
@@ -365,10 +372,29 @@ __global__ __launch_bounds__(256 * NH, 3 - NH) void fwd16_kernel(fa_fwd_params p
              (int64_t)(q_start + m0w) * p.out_stride[2];
   store_rows_staged<Tag, D>(acc, inv, reinterpret_cast<uint16_t*>(smem_raw + wave * C::NDB * 4096), orow0,
                             p.out_stride[2], mrows, lane);
-  if (!mvalid) return;
-  if (h == 0) {
+  if (mvalid && h == 0) {
     float* lb = p.lse + b * p.lse_stride[0] + hq * p.lse_stride[1] + (int64_t)(q_start + m) * p.lse_stride[2];
     *lb = (m_i == kNegInf || l_i == 0.f) ? kNegInf : (m_i + __log2f(l_safe)) * kLn2;
+  }
+  if (end_barrier) __syncthreads();
+}
+
+// PAIR: workgroup (j, bh) runs row block j from the heavy end, then row
+// block j from the light end, of the same (batch, head): under causal
+// masking the two carry the same number of key tiles together, and both
+// read the same head's K / V, which the workgroup's XCD then holds in L2.
+template <typename Tag, int D, int MODE, int NH, bool PAIR>
+__global__ __launch_bounds__(256 * NH, 3 - NH) void fwd16_kernel(fa_fwd_params p, int num_m_blocks) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  if constexpr (!PAIR) {
+    fwd16_item<Tag, D, MODE, NH>(p, num_m_blocks, blockIdx.x, smem_raw, false);
+  } else {
+    const int bh_count = p.batch * p.heads_q;
+    const int j = blockIdx.x / bh_count;
+    const int bh = blockIdx.x - j * bh_count;
+    const int j2 = num_m_blocks - 1 - j;
+    fwd16_item<Tag, D, MODE, NH>(p, num_m_blocks, j * bh_count + bh, smem_raw, j2 != j);
+    if (j2 != j) fwd16_item<Tag, D, MODE, NH>(p, num_m_blocks, j2 * bh_count + bh, smem_raw, false);
   }
 }
 

@@ -273,10 +273,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(fa_fwd_params p, int num_m_blo
     lb[(int64_t)m * p.lse_stride[2]] = (m_i == kNegInf) ? kNegInf : (m_i + __log2f(l_safe)) * kLn2;
 }
 
-template <typename Tag, int D, int MODE, int NH>
+template <typename Tag, int D, int MODE, int NH, bool PAIR = false>
 static hipError_t launch_fwd16(const fa_fwd_params& p, long grid, int nmb, hipStream_t stream) {
   using C = Fwd16Cfg<D, NH>;
-  auto kern = fwd16_kernel<Tag, D, MODE, NH>;
+  auto kern = fwd16_kernel<Tag, D, MODE, NH, PAIR>;
   hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb);
@@ -298,6 +298,11 @@ static hipError_t run_fwd(const fa_fwd_params& p, hipStream_t stream) {
     // orders, so they agree to rounding, not bit for bit.)
     if (p.cu_seqlens_q || grid > 8L * device_cu_count())
       return launch_fwd16<Tag, D, MODE, 1>(p, grid, nmb, stream);
+    // Heavy and light row blocks of a head paired in one workgroup, when
+    // the pairs still give every CU a workgroup (config 2: 256 pairs):
+    // forward 52.5 -> 51.4 us, same results bit for bit.
+    const long pairs = (long)((nmb + 1) / 2) * p.batch * p.heads_q;
+    if (pairs >= device_cu_count()) return launch_fwd16<Tag, D, MODE, 2, true>(p, pairs, nmb, stream);
     return launch_fwd16<Tag, D, MODE, 2>(p, grid, nmb, stream);
     }
   }
