@@ -834,7 +834,6 @@ __global__ __launch_bounds__(512, OCC) void dqs16_kernel(fa_bwd_params p, int nu
   const int m0w = m0 + 32 * wave;
   const int mrows = min(32, sq - m0w);
   const int m = m0w + l32;
-  const bool mvalid = m < sq;
 
   f32x16 dq[C::NDB];
 #pragma unroll
