@@ -778,12 +778,14 @@ struct Dqs16Cfg {
   static_assert(OCC == 1 || 2 * LDS_BYTES <= 160 * 1024, "two workgroups must fit one CU's LDS");
 };
 
+// One work item (query block `item / (B * Hq)` from the heavy end of
+// (batch, head) `item % (B * Hq)`); `end_barrier` as in fwd16_item.
 template <typename Tag, int D, int OCC>
-__global__ __launch_bounds__(512, OCC) void dqs16_kernel(fa_bwd_params p, int num_m_blocks, float dq_scale) {
+__device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blocks, float dq_scale, int item,
+                                           unsigned char* smem_raw, bool end_barrier) {
   using C = Dqs16Cfg<D, OCC>;
   using EL = Elem<Tag>;
   using S = uint16_t;
-  extern __shared__ __align__(16) unsigned char smem_raw[];
   S* smem = reinterpret_cast<S*>(smem_raw);
   const fa_fwd_params& f = p.fwd;
 
@@ -794,8 +796,8 @@ __global__ __launch_bounds__(512, OCC) void dqs16_kernel(fa_bwd_params p, int nu
   const int htid = tid % C::NTH;
   const int h = lane >> 5, l32 = lane & 31;
   const int bh_count = f.batch * f.heads_q;
-  const int mb_rev = blockIdx.x / bh_count;
-  const int bh = blockIdx.x - mb_rev * bh_count;
+  const int mb_rev = item / bh_count;
+  const int bh = item - mb_rev * bh_count;
   const int b = bh / f.heads_q, hq = bh - b * f.heads_q;
   const int hk = hq / (f.heads_q / f.heads_kv);
   const int mblk = num_m_blocks - 1 - mb_rev;  // heaviest causal blocks first
@@ -919,7 +921,10 @@ __global__ __launch_bounds__(512, OCC) void dqs16_kernel(fa_bwd_params p, int nu
       for (int db = 0; db < C::NDB; ++db) park_acc(ow + (wave * C::NDB + db) * 1024, lane, dq[db]);
     }
     __syncthreads();
-    if (khalf == 1) return;
+    if (khalf == 1) {
+      if (end_barrier) __syncthreads();
+      return;
+    }
 #pragma unroll
     for (int db = 0; db < C::NDB; ++db) dq[db] += unpark_acc(ow + (wave * C::NDB + db) * 1024, lane);
   }
@@ -929,6 +934,24 @@ __global__ __launch_bounds__(512, OCC) void dqs16_kernel(fa_bwd_params p, int nu
             (int64_t)(q_start + m0w) * p.dq_stride[2];
   store_rows_staged<Tag, D>(dq, dq_scale, reinterpret_cast<uint16_t*>(smem_raw + wave * C::NDB * 4096), dqr0,
                             p.dq_stride[2], mrows, lane);
+  if (end_barrier) __syncthreads();
+}
+
+// PAIR: workgroup (j, b·Hq) runs query block j from the heavy end, then
+// from the light end, of the same (batch, head), like fwd16_kernel.
+template <typename Tag, int D, int OCC, bool PAIR>
+__global__ __launch_bounds__(512, OCC) void dqs16_kernel(fa_bwd_params p, int num_m_blocks, float dq_scale) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  if constexpr (!PAIR) {
+    dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, blockIdx.x, smem_raw, false);
+  } else {
+    const int bh_count = p.fwd.batch * p.fwd.heads_q;
+    const int j = blockIdx.x / bh_count;
+    const int bh = blockIdx.x - j * bh_count;
+    const int j2 = num_m_blocks - 1 - j;
+    dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, j * bh_count + bh, smem_raw, j2 != j);
+    if (j2 != j) dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, j2 * bh_count + bh, smem_raw, false);
+  }
 }
 
 }  // namespace fa
