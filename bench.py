@@ -224,6 +224,33 @@ def dkdv_roofline(tensors, iters=100):
             "traffic": DKDV_TRAFFIC_BYTES, "avg_us": round(ms * 1e3, 2), "flops_per_launch": flops}
 
 
+def step_kernel_times(tensors, iters=50):
+    """Each kernel of the config-2 step alone, HIP events over `iters`
+    launches on the current stream: forward, delta, dK/dV (stores dS) and
+    dQ from that dS, with the algorithmic TFLOP/s of the three products
+    (forward 4·D, dK/dV 8·D, dQ 2·D flops per visible pair)."""
+    from fa_rdna3 import interface as I
+
+    q, k, v, do, scale = tensors
+    stream = torch.cuda.current_stream()
+    fwd, _ = cfg2_flops()
+    with torch.no_grad():
+        qd, kd, vd = q.detach(), k.detach(), v.detach()
+        run_fwd = lambda: I._forward(qd, kd, vd, True, scale, (-1, -1), 0.0, None, None, 0.0, 0)
+        out, lse = run_fwd()
+        launch = I._backward_launcher(do, qd, kd, vd, out, lse, True, scale, (-1, -1), 0.0, None, None, 0.0, 0)
+        res = {}
+        for name, fn, flops in (("forward", run_fwd, fwd), ("delta", lambda: launch(0), 0.0),
+                                ("dkdv", lambda: launch(1), 2.0 * fwd), ("dq", lambda: launch(2), 0.5 * fwd)):
+            for _ in range(3):
+                fn()
+            ms = _event_time(fn, iters, stream)
+            res[name] = {"us": round(ms * 1e3, 2)}
+            if flops:
+                res[name]["TFLOP/s"] = round(flops / (ms * 1e-3) / 1e12, 1)
+    return res
+
+
 def run_decode_configs(iters=100):
     from fa_rdna3 import (flash_attention_decode, flash_attention_decode_paged, flash_attention_decode_paged_multi,
                           flash_attention_with_kvcache)
@@ -548,6 +575,7 @@ def main():
         "frac_of_peak": round(value / PEAK_FP16_TFLOPS, 4),
     }
     line["roofline"] = dkdv_roofline(tensors)
+    line["cfg2_kernels"] = step_kernel_times(tensors)
     if not args.no_extras:
         ceil = gemm_ceiling()
         line["mfma_gemm_ceiling"] = {
