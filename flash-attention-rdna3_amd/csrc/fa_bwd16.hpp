@@ -49,9 +49,6 @@ __device__ inline int64_t ds_region(const fa_bwd_params& p, int b, int hq, int s
 // ---------------------------------------------------------------------------
 // dK / dV: each wave owns 32 keys (lane axis of S = Q K^T).
 // ---------------------------------------------------------------------------
-#ifndef FA_DQ_OCC
-#define FA_DQ_OCC 2
-#endif
 // A workgroup owns BN = 128 keys (32 per wave of a half) and splits their
 // query range in two: waves 0-3 walk the first half of the query steps,
 // waves 4-7 the second, each half through its own double-buffered Q / dO

@@ -343,20 +343,6 @@ __device__ inline void dispatch_mods(const Mods& md, F&& f) {
   else { if (al) with_bias(N{}, T{}); else with_bias(N{}, N{}); }
 }
 
-// Order of query blocks over the grid for kernels whose block cost grows with
-// the block index (causal attention): block slot `idx` of `nb` maps to the
-// heaviest half descending, then the lightest half ascending.  When the whole
-// grid is resident at once (two workgroups per CU), the k-th and (k+G/2)-th
-// workgroups share a CU, so heavy blocks are paired with light ones.
-#ifndef FA_BLOCK_ORDER
-#define FA_BLOCK_ORDER 1
-#endif
-__device__ inline int causal_block(int idx, int nb) {
-  if (FA_BLOCK_ORDER == 0) return nb - 1 - idx;
-  const int half = (nb + 1) / 2;
-  return idx < half ? nb - 1 - idx : idx - half;
-}
-
 __device__ inline bool dropout_keep(const Mods& md, int m, int n) {
   const uint64_t o = (md.drop_base + (uint64_t)m) * (uint64_t)md.drop_sk + (uint64_t)n;
   return philox_uniform(md.drop_seed, o) > md.drop_p;

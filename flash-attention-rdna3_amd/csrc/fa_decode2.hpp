@@ -52,10 +52,9 @@ struct Dec2Cfg {
   static constexpr int KLOADS = 2 * NSTEP;           // K dwordx4 loads per chunk per lane
   static constexpr int VLOADS = CK * CPR / 64;       // V dwordx4 loads per chunk per lane
   static constexpr int PER = KLOADS + VLOADS;        // vector-memory ops per chunk
-  // Chunk slots per wave (each slot is 4*PER VGPRs per lane).
-#ifndef FA_DEC_SLOT_VGPRS
-#define FA_DEC_SLOT_VGPRS 128
-#endif
+  // Chunk slots per wave (each slot is 4*PER VGPRs per lane): 128 VGPRs of
+  // slots for 16-bit caches, 64 for fp8 caches (SLOT_VGPRS8).
+  static constexpr int SLOT_VGPRS = 128;
   // fp8 cache: 16-byte loads of 16 elements.  K steps go in pairs (KP) when
   // NSTEP is even (else one 8-byte load per step); V rows in 16-element
   // pieces (VN loads per chunk per lane).
@@ -63,10 +62,8 @@ struct Dec2Cfg {
   static constexpr int KN = KP ? NSTEP / 2 : NSTEP;   // K loads per key block
   static constexpr int VN = KV8 ? CK * (D / 16) / 64 : VLOADS;
   static constexpr int SLOT_REGS = KV8 ? 2 * KN * (KP ? 4 : 2) + 4 * VN : 4 * PER;
-#ifndef FA_DEC_SLOT_VGPRS8
-#define FA_DEC_SLOT_VGPRS8 64
-#endif
-  static constexpr int NBUF = (KV8 ? FA_DEC_SLOT_VGPRS8 : WIDE ? 64 : FA_DEC_SLOT_VGPRS) / SLOT_REGS;
+  static constexpr int SLOT_VGPRS8 = 64;
+  static constexpr int NBUF = (KV8 ? SLOT_VGPRS8 : WIDE ? 64 : SLOT_VGPRS) / SLOT_REGS;
   static constexpr int WAVE_ELEMS = TILE;            // one private V tile per wave
   static constexpr int LOOP_BYTES = NW * WAVE_ELEMS * 2;
   static constexpr int OLD = 17;                     // merge buffer row stride (floats)
@@ -268,20 +265,6 @@ __global__ __launch_bounds__((KV8 || PAGE == 2) ? 512 : 256) void decode2_kernel
     }
   };
   auto compute_chunk = [&](int c, const KRaw (&kd)[2][C::KN], const VRaw (&vd)[C::VN]) {
-#ifdef FA_DEC_EXP
-    if constexpr (!KV8) {
-      uint32_t x = 0;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int s2 = 0; s2 < C::KN; ++s2) { const u32x4 w = __builtin_bit_cast(u32x4, kd[kb][s2]); x ^= w[0] ^ w[1] ^ w[2] ^ w[3]; }
-#pragma unroll
-      for (int i = 0; i < C::VN; ++i) { const u32x4 w = __builtin_bit_cast(u32x4, vd[i]); x ^= w[0] ^ w[1] ^ w[2] ^ w[3]; }
-      acc[0][0] += __uint_as_float(x & 0x3fffffffu) * 1e-30f;
-      l_i = 1.f; m_i = 0.f;
-      return;
-    }
-#endif
     const uint32_t vmask = chunk_mask(c);
     // V rows -> this wave's LDS tile (swizzled); the previous chunk's reads of
     // the tile precede these writes in the wave's LDS order.
