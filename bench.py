@@ -376,24 +376,46 @@ def run_decode_configs(iters=100):
                                 "caches_flushed": "read of 512 MiB", "bytes": br,
                                 "shape": "B=16 lengths 64..32768 (sum 71780), Hq 32, Hkv 8, D 128, fp16"}
         del qr, kr, vr
-        # Context for frac_hbm: what a plain library read of the same number
-        # of bytes reaches on this box (torch max-reduction, caches flushed).
-        # It is a reference point, not a ceiling: a hand-written streaming read
-        # does better.
-        ceil = {}
-        for name, nbytes in (("cfg3_bytes", cfg3_bytes(lens.tolist())), ("cfg4_bytes", cfg4_bytes())):
-            x = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+        res["hbm_read_ceiling"] = hbm_read_ceiling(
+            {"cfg3_bytes": cfg3_bytes(lens.tolist()), "cfg4_bytes": cfg4_bytes()}, flush, iters)
+        for name, key in (("cfg3_splitk_decode", "cfg3_bytes"), ("cfg4_paged_decode", "cfg4_bytes")):
+            res[name]["frac_of_read_ceiling"] = round(res["hbm_read_ceiling"][key]["us"] / res[name]["us"], 4)
+    return res
+
+
+def hbm_read_ceiling(sizes, flush, iters=50):
+    """The HBM read rate a plain hand-written streaming kernel reaches for
+    each byte count (fa_hbm_read_probe: every 16-byte piece read once, U
+    loads per lane in flight), caches flushed before every timed call; the
+    best of the probe's variants (block size, loads in flight, nontemporal,
+    one-pass or persistent grid) is the ceiling."""
+    from fa_rdna3 import _native
+
+    stream = torch.cuda.current_stream()
+    sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    names = _native.hbm_read_probe_variants()
+    out = {}
+    for key, nbytes in sizes.items():
+        x = torch.ones((nbytes + 15) // 16 * 4, dtype=torch.int32, device="cuda")
+        best = None
+        for vi in range(len(names)):
+            fn = lambda: _native.hbm_read_probe(x, sink, vi)
             for _ in range(3):
-                x.max()
+                fn()
             tot = 0.0
             for _ in range(iters):
                 _flush(flush)
-                tot += _event_time(lambda: x.max(), 1, stream)
-            ms = tot / iters
-            ceil[name] = {"bytes": nbytes, "us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
-            del x
-        res["torch_read_reference"] = dict(ceil, how="torch int32 max-reduction over the same byte count, caches flushed")
-    return res
+                tot += _event_time(fn, 1, stream)
+            us = tot / iters * 1e3
+            if best is None or us < best[0]:
+                best = (us, vi)
+        us, vi = best
+        out[key] = {"bytes": nbytes, "us": round(us, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                    "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "variant": names[vi]}
+        del x
+    out["how"] = ("fa_hbm_read_probe (csrc/fa_hbm_read.hip), best of its variants, HIP events, "
+                  "512 MiB read before every call")
+    return out
 
 
 def run_cfg5(iters=20):
@@ -423,6 +445,33 @@ def run_cfg5(iters=20):
     dt = (time.perf_counter() - t0) / iters
     fwd, bwd = cfg5_flops(lengths)
     return {"ms": round(dt * 1e3, 3), "TFLOP/s": round((fwd + bwd) / dt / 1e12, 1)}
+
+
+def run_long_causal(iters=5):
+    """A long causal sequence: B=1, H=32, S=16384, D=128 fp16 fwd + bwd
+    (7.70 TFLOP by the cfg2 convention), warmed up, then `iters` steps."""
+    from fa_rdna3 import flash_attention
+
+    g = _gen(4)
+    shape = (1, 32, 16384, 128)
+    q, k, v, do = (torch.randn(shape, generator=g).half().cuda() for _ in range(4))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        flash_attention(q, k, v, causal=True).backward(do)
+
+    step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / iters
+    fwd = 4.0 * 32 * 16384 ** 2 * 128 / 2
+    return {"ms": round(dt * 1e3, 3), "TFLOP/s": round(3.5 * fwd / dt / 1e12, 1),
+            "shape": "B=1 H=32 S=16384 D=128 fp16 causal fwd+bwd"}
 
 
 def _cpu_model():
@@ -478,6 +527,138 @@ def cpu_baseline(budget_s=20.0):
             "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": threads}
 
 
+def _cpu_median(run, budget_s):
+    """Median wall time of run() over 5 timed calls after 3 warm-ups (one
+    untimed call first pays one-time set-up)."""
+    run()
+    times = []
+    for i in range(8):
+        t0 = time.perf_counter()
+        run()
+        if i >= 3:
+            times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def _cpu_attention(q, k, v, scale, causal=False, window_left=-1, softcap=0.0):
+    """fp32 math attention on the host, (H, Sq, D) x (Hkv, Sk, D), GQA by
+    head groups, bottom-right causal, left window, tanh softcap: the
+    matmul -> softmax -> matmul path of the reference's CPU comparison.
+    Returns (out, lse)."""
+    hq, sq, d = q.shape
+    hk, sk = k.shape[0], k.shape[1]
+    qg = q.reshape(hk, (hq // hk) * sq, d)
+    s = torch.matmul(qg, k.transpose(-1, -2)).reshape(hq, sq, sk) * scale
+    if softcap > 0:
+        s = softcap * torch.tanh(s / softcap)
+    if causal or window_left >= 0:
+        i = torch.arange(sq)[:, None] + (sk - sq)
+        j = torch.arange(sk)[None, :]
+        keep = torch.ones(sq, sk, dtype=torch.bool)
+        if causal:
+            keep &= j <= i
+        if window_left >= 0:
+            keep &= j >= i - window_left
+        s = s.masked_fill(~keep, float("-inf"))
+    lse = torch.logsumexp(s, dim=-1)
+    p = torch.exp(s - lse[..., None])
+    out = torch.matmul(p.reshape(hk, (hq // hk) * sq, sk), v).reshape(hq, sq, d)
+    return out, lse
+
+
+def cpu_baseline_configs(budget_s=8.0):
+    """The reference's CPU path (fp32 math attention, reference
+    bench/benchmark.py:69,116 and bench/decode_benchmark.py:56-57) on the
+    other BASELINE configurations, on the host cores, inputs already in fp32
+    host memory:
+      cfg1  forward with out + LSE (the configuration that is the CPU path);
+      cfg3  split-K GQA decode: per sequence, the first cache_seqlens keys;
+      cfg4  paged decode: the block table's pages gathered, then attended
+            (the gather is inside the timed region);
+      cfg5  varlen causal fwd + autograd bwd with window 1024 and softcap 50,
+            on a leading slice of the sequences sized to the budget.
+    Rates use the GPU bench's algorithmic units (GFLOP/s; GB/s of the fp16
+    K/V bytes of the workload, whatever width the CPU reads)."""
+    res = {}
+    torch.manual_seed(0)
+    # cfg1
+    q, k, v, scale = workload_cfg1()
+    q, k, v = q[0], k[0], v[0]
+    with torch.no_grad():
+        t = _cpu_median(lambda: _cpu_attention(q, k, v, scale), budget_s)
+    flops = 4.0 * 16 * 1024 * 1024 * 64
+    res["cfg1_fwd"] = {"value": round(flops / t / 1e9, 2), "unit": "GFLOP/s", "ms": round(t * 1e3, 2),
+                       "sample": "full cfg1: B=1 H=16 S=1024 D=64 fp32, non-causal, out + LSE"}
+    # cfg3
+    q, k, v, lens = workload_cfg3("cpu")
+    q, k, v = q.float(), k.float(), v.float()
+    lens = lens.tolist()
+
+    def dec3():
+        for b, n in enumerate(lens):
+            _cpu_attention(q[b], k[b, :, :n], v[b, :, :n], 1.0 / math.sqrt(128))
+
+    with torch.no_grad():
+        t = _cpu_median(dec3, budget_s)
+    res["cfg3_decode"] = {"value": round(cfg3_bytes(lens) / t / 1e9, 2), "unit": "GB/s", "ms": round(t * 1e3, 2),
+                          "sample": "full cfg3: 4 sequences, Hq 32 / Hkv 8, cache_seqlens [5713, 6857, 7358, 7415], "
+                                    "fp32 cache in host memory"}
+    del q, k, v
+    # cfg4
+    q, kc, vc, bt, ctx = workload_cfg4("cpu")
+    q, kc, vc = q.float(), kc.float(), vc.float()
+
+    def dec4():
+        for b in range(4):
+            pages = bt[b].long()
+            kk = kc.index_select(0, pages).reshape(-1, 8, 128)[: int(ctx[b])].transpose(0, 1)
+            vv = vc.index_select(0, pages).reshape(-1, 8, 128)[: int(ctx[b])].transpose(0, 1)
+            _cpu_attention(q[b][:, None], kk, vv, 1.0 / math.sqrt(128))
+
+    with torch.no_grad():
+        t = _cpu_median(dec4, budget_s)
+    res["cfg4_paged_decode"] = {"value": round(cfg4_bytes() / t / 1e9, 2), "unit": "GB/s", "ms": round(t * 1e3, 2),
+                                "sample": "full cfg4: 4 x 16384 keys in 16-key pages, Hq 32 / Hkv 8, gather + attend, "
+                                          "fp32 cache in host memory"}
+    del q, kc, vc
+    # cfg5: the first sequence, on as many KV-head groups (4 query heads
+    # each) as fit the budget
+    lengths, q, k, v, do, cu = workload_cfg5("cpu")
+    q, k, v, do = q.float(), k.float(), v.float(), do.float()
+    n0 = lengths[0]
+
+    def varlen(hk):
+        qs = q[:n0, :4 * hk].transpose(0, 1).clone().requires_grad_(True)
+        ks = k[:n0, :hk].transpose(0, 1).clone().requires_grad_(True)
+        vs = v[:n0, :hk].transpose(0, 1).clone().requires_grad_(True)
+        out, _ = _cpu_attention(qs, ks, vs, 1.0 / math.sqrt(128), causal=True, window_left=1024, softcap=50.0)
+        out.backward(do[:n0, :4 * hk].transpose(0, 1))
+
+    varlen(1)
+    t0 = time.perf_counter()
+    varlen(1)
+    one = time.perf_counter() - t0
+    hk = max(1, min(8, int(budget_s / 6 / max(one, 1e-3))))
+    times = []
+    for i in range(4):
+        t0 = time.perf_counter()
+        varlen(hk)
+        if i >= 1:
+            times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    fwd, bwd = cfg5_flops(lengths[:1])
+    frac = hk / 8
+    res["cfg5_varlen_fwd_bwd"] = {"value": round((fwd + bwd) * frac / t / 1e9, 2), "unit": "GFLOP/s",
+                                  "ms": round(t * 1e3, 2),
+                                  "sample": f"first cfg5 sequence ({n0} tokens), {4 * hk} of 32 query heads "
+                                            f"({hk} of 8 KV heads), D 128 fp32, causal, window 1024, softcap 50, "
+                                            "fwd + autograd bwd; median of 3 after 1 warm-up"}
+    for r in res.values():
+        r["cores"] = torch.get_num_threads()
+        r["kind"] = "reference"
+    return res
+
+
 def pmc_summary(dirs):
     """Markdown table of rocprofv3 --pmc results (one directory per counter
     pass, each holding run_results.db): per kernel and grid, the average per
@@ -524,6 +705,45 @@ def pmc_summary(dirs):
         print(f"| `{name}` | {grid} | " + " | ".join(f"{c[n]:.4g}" if n in c else "" for n in names) + " |")
 
 
+def traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mib=256):
+    """Markdown table of HBM bytes per dispatch from rocprofv3 --pmc
+    FETCH_SIZE and WRITE_SIZE runs (--output-format csv), one directory per
+    counter, each scaled by what the same counter reads for a device copy of
+    copy_mib MiB (bench.py --copy-calibration)."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    def means(d, only_fa=True):
+        acc = defaultdict(list)
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                name = r["Kernel_Name"]
+                if only_fa and "fa::" not in name:
+                    continue
+                key = (name.split("(")[0].replace("void fa::", "").replace("fa::", ""), int(r.get("Grid_Size", 0)))
+                acc[key].append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in acc.items()}
+
+    def copy_kib(d):
+        vals = [v for (n, _), v in means(d, only_fa=False).items() if "copyBuffer" in n or "copy" in n.lower()]
+        return max(vals) if vals else None
+
+    n = copy_mib * 1024 * 1024
+    cf, cw = copy_kib(copy_fetch_dir), copy_kib(copy_write_dir)
+    fs, ws = n / (cf * 1024), n / (cw * 1024)
+    fetch, write = means(fetch_dir), means(write_dir)
+    print(f"Calibration, {copy_mib} MiB device copy: FETCH_SIZE {cf:.0f} KiB per dispatch -> x{fs:.2f} to bytes read; "
+          f"WRITE_SIZE {cw:.0f} KiB -> x{ws:.2f} to bytes written.")
+    print()
+    print("| kernel | grid | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM read MB | HBM write MB | total MB |")
+    print("|---|---|---|---|---|---|---|")
+    for key in sorted(set(fetch) | set(write), key=lambda k: -fetch.get(k, 0.0)):
+        f, w = fetch.get(key, 0.0), write.get(key, 0.0)
+        rd, wr = f * 1024 * fs / 1e6, w * 1024 * ws / 1e6
+        print(f"| `{key[0]}` | {key[1]} | {f:.0f} | {w:.0f} | {rd:.1f} | {wr:.1f} | {rd + wr:.1f} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -535,9 +755,19 @@ def main():
                     help="only run 10 device copies of MIB MiB (scales rocprofv3 FETCH/WRITE_SIZE)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="only summarise rocprofv3 --pmc result directories as markdown")
+    ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
+                    help="only summarise rocprofv3 FETCH_SIZE / WRITE_SIZE csv directories as HBM bytes")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only run the decode measurements (a few calls each) and print them")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(args.pmc_summary)
+        return
+    if args.traffic_summary:
+        traffic_summary(*args.traffic_summary)
+        return
+    if args.decode_only:
+        print(json.dumps(run_decode_configs(iters=max(1, args.steps))), flush=True)
         return
     if args.copy_calibration:
         n = args.copy_calibration * 1024 * 1024
@@ -583,8 +813,10 @@ def main():
             "step_frac": round(value / ceil, 4), "dkdv_frac": round(line["roofline"]["achieved"] / ceil, 4)}
         line["decode"] = run_decode_configs()
         line["cfg5_varlen"] = run_cfg5()
+        line["long_causal"] = run_long_causal()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
+        line["cpu_baseline_configs"] = cpu_baseline_configs()
     print(json.dumps(line), flush=True)
 
 

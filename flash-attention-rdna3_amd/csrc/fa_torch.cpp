@@ -22,6 +22,7 @@
 // messages before any of these is called; the C ABI re-checks what could
 // make a kernel access memory out of bounds.
 #include <ATen/ATen.h>
+#include <ATen/core/dispatch/Dispatcher.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/autograd.h>
@@ -254,12 +255,49 @@ std::tuple<Tensor, Tensor, Tensor> backward_op(const Tensor& dout, const Tensor&
 
 // Autograd of the dense attention: q, k, v differentiable; bias and ALiBi
 // slopes are not (reference interface.py:316-333).
+// Shape functions of forward / backward (Meta kernels): FakeTensorMode,
+// make_fx and other tracers run these instead of the launches.
+std::tuple<Tensor, Tensor> forward_meta(const Tensor& q, const Tensor& k, const Tensor& v, bool causal, double scale,
+                                        int64_t wl, int64_t wr, double softcap, const OptTensor& bias,
+                                        const OptTensor& alibi, double dropout_p, int64_t seed) {
+  return {at::empty(q.sizes(), q.options()), at::empty({q.size(0), q.size(1), q.size(2)}, q.options().dtype(at::kFloat))};
+}
+
+std::tuple<Tensor, Tensor, Tensor> backward_meta(const Tensor& dout, const Tensor& q, const Tensor& k,
+                                                 const Tensor& v, const Tensor& out, const Tensor& lse, bool causal,
+                                                 double scale, int64_t wl, int64_t wr, double softcap,
+                                                 const OptTensor& bias, const OptTensor& alibi, double dropout_p,
+                                                 int64_t seed) {
+  return {at::empty(q.sizes(), q.options()), at::empty(k.sizes(), k.options()), at::empty(v.sizes(), v.options())};
+}
+
+// The autograd function calls forward / backward through the dispatcher, so
+// a tracer (FakeTensorMode, make_fx) sees those operators and their Meta
+// kernels rather than raw launches on its tensors.
+std::tuple<Tensor, Tensor> call_forward(const Tensor& q, const Tensor& k, const Tensor& v, const Options& o) {
+  static const auto op = c10::Dispatcher::singleton()
+                             .findSchemaOrThrow("fa_mi355x::forward", "")
+                             .typed<decltype(forward_op)>();
+  return op.call(q, k, v, o.causal, o.scale, o.window_left, o.window_right, o.softcap, o.bias, o.alibi, o.dropout_p,
+                 o.dropout_seed);
+}
+
+std::tuple<Tensor, Tensor, Tensor> call_backward(const Tensor& dout, const Tensor& q, const Tensor& k,
+                                                 const Tensor& v, const Tensor& out, const Tensor& lse,
+                                                 const Options& o) {
+  static const auto op = c10::Dispatcher::singleton()
+                             .findSchemaOrThrow("fa_mi355x::backward", "")
+                             .typed<decltype(backward_op)>();
+  return op.call(dout, q, k, v, out, lse, o.causal, o.scale, o.window_left, o.window_right, o.softcap, o.bias,
+                 o.alibi, o.dropout_p, o.dropout_seed);
+}
+
 class AttentionFn : public torch::autograd::Function<AttentionFn> {
  public:
   static Tensor forward(torch::autograd::AutogradContext* ctx, const Tensor& q, const Tensor& k, const Tensor& v,
                         bool causal, double scale, int64_t wl, int64_t wr, double softcap, const OptTensor& bias,
                         const OptTensor& alibi, double dropout_p, int64_t seed) {
-    auto [out, lse] = forward_impl(q, k, v, make_options(causal, scale, wl, wr, softcap, bias, alibi, dropout_p, seed));
+    auto [out, lse] = call_forward(q, k, v, make_options(causal, scale, wl, wr, softcap, bias, alibi, dropout_p, seed));
     ctx->save_for_backward({q, k, v, out, lse, bias.value_or(Tensor()), alibi.value_or(Tensor())});
     ctx->saved_data["causal"] = causal;
     ctx->saved_data["scale"] = scale;
@@ -286,7 +324,7 @@ class AttentionFn : public torch::autograd::Function<AttentionFn> {
               alibi.defined() ? OptTensor(alibi) : std::nullopt,
               ctx->saved_data["dropout_p"].toDouble(),
               ctx->saved_data["seed"].toInt()};
-    auto [dq, dk, dv] = backward_impl(grads[0], saved[0], saved[1], saved[2], saved[3], saved[4], o);
+    auto [dq, dk, dv] = call_backward(grads[0], saved[0], saved[1], saved[2], saved[3], saved[4], o);
     return {dq, dk, dv, Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
   }
 };
@@ -322,4 +360,9 @@ TORCH_LIBRARY_IMPL(fa_mi355x, CompositeImplicitAutograd, m) { m.impl("attention"
 TORCH_LIBRARY_IMPL(fa_mi355x, CUDA, m) {
   m.impl("forward", &forward_op);
   m.impl("backward", &backward_op);
+}
+
+TORCH_LIBRARY_IMPL(fa_mi355x, Meta, m) {
+  m.impl("forward", &forward_meta);
+  m.impl("backward", &backward_meta);
 }

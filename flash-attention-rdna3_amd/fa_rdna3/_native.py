@@ -128,6 +128,7 @@ EXPORTS = (
     "fa_fwd", "fa_bwd", "fa_bwd_phase", "fa_bwd_workspace_bytes", "fa_decode_splitk", "fa_decode_splitk_noalloc", "fa_decode_paged",
     "fa_tiny_fwd_f32",
     "fa_kvcache_append",
+    "fa_hbm_read_probe_count", "fa_hbm_read_probe_name", "fa_hbm_read_probe",
 )
 
 _lib = None
@@ -170,6 +171,12 @@ def lib():
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(struct), ctypes.c_void_p]
         handle.fa_bwd_phase.restype = ctypes.c_int
+        handle.fa_hbm_read_probe_count.restype = ctypes.c_int
+        handle.fa_hbm_read_probe_name.restype = ctypes.c_char_p
+        handle.fa_hbm_read_probe_name.argtypes = [ctypes.c_int]
+        handle.fa_hbm_read_probe.restype = ctypes.c_int
+        handle.fa_hbm_read_probe.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                             ctypes.c_void_p]
         handle.fa_bwd_phase.argtypes = [ctypes.POINTER(BwdParams), ctypes.c_int, ctypes.c_void_p]
         if handle.fa_abi_version() != ABI_VERSION:
             raise RuntimeError(f"{_LIB_NAME} ABI {handle.fa_abi_version()} != binding ABI {ABI_VERSION}")
@@ -262,7 +269,15 @@ def decode_tickets(device_tensor, batch, heads_q, seqlen_q):
 
     The decode kernels leave every counter at zero, so one buffer per
     (device, stream) serves all calls issued in stream order; it grows when
-    a call needs more counters than it holds."""
+    a call needs more counters than it holds.
+
+    Under HIP graph capture no buffer is created: a capture only records the
+    zero fill, so a buffer made then would hold undefined counters for
+    every later eager call or other graph on that stream.  A call captured
+    before its stream has a large enough buffer therefore takes the
+    two-launch merge (None).  A buffer that a graph may have recorded is
+    never freed: when a larger one replaces it, the old one is kept alive
+    for the life of the process."""
     if not FUSED_SPLIT_MERGE:
         return None
     need = int(lib().fa_decode_ticket_count(batch, heads_q, seqlen_q))
@@ -270,10 +285,17 @@ def decode_tickets(device_tensor, batch, heads_q, seqlen_q):
     key = (device_tensor.device.index, stream.cuda_stream)
     buf = _tickets.get(key)
     if buf is None or buf.numel() < need:
+        if torch.cuda.is_current_stream_capturing():
+            return None
         size = max(need, 1024 if buf is None else 2 * buf.numel())
+        if buf is not None:
+            _retired_tickets.append(buf)
         buf = torch.zeros(size, dtype=torch.int32, device=device_tensor.device)
         _tickets[key] = buf
     return buf.data_ptr()
+
+
+_retired_tickets = []
 
 
 def kernel_ready(t):
@@ -294,3 +316,18 @@ def strides(t, n=None):
     st = [s if sz > 1 else 0 for s, sz in zip(t.stride(), t.shape)]
     st[-1] = 1
     return st if n is None else st[:n]
+
+
+def hbm_read_probe(src, sink, variant):
+    """Read every byte of the device tensor ``src`` once with the streaming
+    read probe ``variant`` on the current stream (``sink``: >= 4 KiB of
+    device memory).  A measurement utility, not part of the attention path."""
+    nbytes = src.numel() * src.element_size()
+    _check(lib().fa_hbm_read_probe(src.data_ptr(), nbytes, sink.data_ptr(), int(variant), _stream(src)),
+           "fa_hbm_read_probe")
+
+
+def hbm_read_probe_variants():
+    """Descriptions of the streaming read probe's variants, by index."""
+    n = lib().fa_hbm_read_probe_count()
+    return [lib().fa_hbm_read_probe_name(i).decode() for i in range(n)]

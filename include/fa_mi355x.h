@@ -349,6 +349,20 @@ int fa_decode_splitk(const fa_decode_params* params, void* stream);
 #define FA_NOALLOC_TICKETS 65536
 int fa_decode_splitk_noalloc(const fa_decode_params* params, void* stream);
 int fa_decode_paged(const fa_paged_params* params, void* stream);
+
+/*
+ * HBM streaming-read probe.  No counterpart in the reference: it is the
+ * measurement the HBM-bound decode kernels are compared against.  Reads
+ * every byte of [src, src + bytes) once with 16-byte loads (bytes a multiple
+ * of 16, src 16-byte aligned) and writes at most a few bytes of `sink`
+ * (>= 4 KiB of device memory).  `variant` in [0, fa_hbm_read_probe_count())
+ * picks the block size, loads in flight per lane, plain or nontemporal loads,
+ * and one-pass or persistent grid; fa_hbm_read_probe_name describes it.
+ * Returns 0, or 1 for bad arguments, 3 for a launch failure.
+ */
+int fa_hbm_read_probe_count(void);
+const char* fa_hbm_read_probe_name(int variant);
+int fa_hbm_read_probe(const void* src, size_t bytes, void* sink, int variant, void* stream);
 int fa_tiny_fwd_f32(const fa_tiny_params* params, void* stream);
 int fa_kvcache_append(const fa_append_params* params, void* stream);
 
