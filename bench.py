@@ -705,6 +705,22 @@ def pmc_summary(dirs):
         print(f"| `{name}` | {grid} | " + " | ".join(f"{c[n]:.4g}" if n in c else "" for n in names) + " |")
 
 
+def stats_summary(d):
+    """Markdown table of a rocprofv3 --kernel-trace --stats run
+    (--output-format csv): calls, average and total time per kernel."""
+    import csv
+    import glob
+
+    f = glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)[0]
+    rows = list(csv.DictReader(open(f)))
+    print("| kernel | calls | avg us | total us | % |")
+    print("|---|---|---|---|---|")
+    for r in rows:
+        name = r["Name"] if len(r["Name"]) <= 100 else r["Name"][:100] + "…"
+        print(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['TotalDurationNs']) / 1e3:.1f} "
+              f"| {float(r['Percentage']):.1f} |")
+
+
 def traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mib=256):
     """Markdown table of HBM bytes per dispatch from rocprofv3 --pmc
     FETCH_SIZE and WRITE_SIZE runs (--output-format csv), one directory per
@@ -757,11 +773,16 @@ def main():
                     help="only summarise rocprofv3 --pmc result directories as markdown")
     ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
                     help="only summarise rocprofv3 FETCH_SIZE / WRITE_SIZE csv directories as HBM bytes")
+    ap.add_argument("--stats-summary", metavar="DIR",
+                    help="only summarise a rocprofv3 --kernel-trace --stats csv directory as markdown")
     ap.add_argument("--decode-only", action="store_true",
                     help="only run the decode measurements (a few calls each) and print them")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(args.pmc_summary)
+        return
+    if args.stats_summary:
+        stats_summary(args.stats_summary)
         return
     if args.traffic_summary:
         traffic_summary(*args.traffic_summary)

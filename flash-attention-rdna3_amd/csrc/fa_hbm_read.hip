@@ -7,10 +7,14 @@
 // with dwordx4 loads, keeps U loads per lane in flight before it uses any of
 // them, folds them into one XOR per lane and stores that only when it equals
 // a value the data never produce, so the loads cannot be elided and almost
-// nothing is written.  Two grid shapes:
+// nothing is written.  Three grid shapes:
 //   * one pass: workgroup i reads the contiguous span [i * NT * U, (i + 1) * NT * U)
-//     pieces (the decode kernels' shape: each workgroup reads its own range);
-//   * persistent: 8 workgroups per CU walk the spans in a grid-stride loop.
+//     pieces, and the hardware hands spans to CUs as workgroups finish;
+//   * grid-stride: a fixed number of workgroups per CU walk the spans in a
+//     grid-stride loop (all of them advance through the buffer together);
+//   * contiguous slices: a fixed number of workgroups per CU each walk their
+//     own contiguous slice (one long stream per workgroup, as the split-K
+//     decode reads its key ranges).
 // Plain or nontemporal loads.
 #include <hip/hip_runtime.h>
 
@@ -23,13 +27,17 @@ namespace fa {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-template <int NT, int U, bool NTL, bool PERSIST>
+template <int NT, int U, bool NTL, int PERSIST>
 __global__ __launch_bounds__(NT) void hbm_read_kernel(const u32x4_t* __restrict__ src, int64_t n16,
                                                       uint32_t* __restrict__ sink) {
   constexpr int64_t SPAN = (int64_t)NT * U;
   const int64_t nspan = (n16 + SPAN - 1) / SPAN;
   uint32_t acc = 0;
-  for (int64_t sp = blockIdx.x; sp < nspan; sp += PERSIST ? gridDim.x : nspan) {
+  // PERSIST 2: workgroup i walks its own contiguous slice of the spans.
+  const int64_t per = (nspan + gridDim.x - 1) / gridDim.x;
+  const int64_t sp0 = PERSIST == 2 ? blockIdx.x * per : blockIdx.x;
+  const int64_t sp1 = PERSIST == 2 ? (sp0 + per < nspan ? sp0 + per : nspan) : nspan;
+  for (int64_t sp = sp0; sp < sp1; sp += PERSIST == 1 ? gridDim.x : PERSIST == 2 ? 1 : nspan) {
     const int64_t base = sp * SPAN + threadIdx.x;
     u32x4_t v[U];
 #pragma unroll
@@ -48,18 +56,21 @@ __global__ __launch_bounds__(NT) void hbm_read_kernel(const u32x4_t* __restrict_
 struct ReadVariant {
   const void* fn;
   int nt, u;
-  bool persist;
+  int persist;  // 0 one pass, 1 grid-stride (8 per CU), 2 contiguous slices (persist_wg per CU)
+  int per_cu;
   const char* name;
 };
 
-#define FA_RV(NT, U, NTL, P) \
-  { (const void*)hbm_read_kernel<NT, U, NTL, P>, NT, U, P, #NT " threads, " #U " x 16 B per lane in flight, " \
-    #NTL " nontemporal, " #P " persistent" }
+#define FA_RV(NT, U, NTL, P, C) \
+  { (const void*)hbm_read_kernel<NT, U, NTL, P>, NT, U, P, C, #NT " threads, " #U " x 16 B per lane in flight, " \
+    #NTL " nontemporal, grid mode " #P " (0 one pass, 1 grid-stride, 2 contiguous slices), " #C " per CU" }
 static const ReadVariant kReadVariants[] = {
-    FA_RV(256, 8, false, false),  FA_RV(256, 16, false, false), FA_RV(512, 8, false, false),
-    FA_RV(512, 16, false, false), FA_RV(1024, 8, false, false), FA_RV(256, 8, true, false),
-    FA_RV(256, 16, true, false),  FA_RV(512, 8, true, false),   FA_RV(256, 8, false, true),
-    FA_RV(256, 16, false, true),  FA_RV(512, 8, false, true),   FA_RV(256, 16, true, true),
+    FA_RV(256, 8, false, 0, 0),  FA_RV(256, 16, false, 0, 0), FA_RV(512, 8, false, 0, 0),
+    FA_RV(512, 16, false, 0, 0), FA_RV(1024, 8, false, 0, 0), FA_RV(256, 8, true, 0, 0),
+    FA_RV(256, 16, true, 0, 0),  FA_RV(512, 8, true, 0, 0),   FA_RV(256, 8, false, 1, 8),
+    FA_RV(256, 16, false, 1, 8), FA_RV(512, 8, false, 1, 8),  FA_RV(256, 16, true, 1, 8),
+    FA_RV(256, 8, true, 2, 1),   FA_RV(256, 8, true, 2, 2),   FA_RV(256, 8, true, 2, 8),
+    FA_RV(256, 16, true, 2, 1),
 };
 #undef FA_RV
 constexpr int kNumReadVariants = sizeof(kReadVariants) / sizeof(kReadVariants[0]);
@@ -81,7 +92,7 @@ int fa_hbm_read_probe(const void* src, size_t bytes, void* sink, int variant, vo
   const int64_t n16 = (int64_t)(bytes / 16);
   const int64_t span = (int64_t)rv.nt * rv.u;
   const int64_t nspan = (n16 + span - 1) / span;
-  const int64_t grid = rv.persist ? std::min<int64_t>(nspan, 8 * (int64_t)fa::device_cu_count()) : nspan;
+  const int64_t grid = rv.persist ? std::min<int64_t>(nspan, rv.per_cu * (int64_t)fa::device_cu_count()) : nspan;
   if (grid > 0x7FFFFFFF) return 1;
   const fa::u32x4_t* s = reinterpret_cast<const fa::u32x4_t*>(src);
   uint32_t* k = reinterpret_cast<uint32_t*>(sink);

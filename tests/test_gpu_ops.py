@@ -284,16 +284,18 @@ def test_dispatch_defers_causal_with_mask_to_original():
     mask = torch.ones(4, 4, device=DEVICE, dtype=torch.bool)
     original = F.scaled_dot_product_attention
     try:
-        expected, expected_exc = original(q, q, q, attn_mask=mask, is_causal=True), None
+        original(q, q, q, attn_mask=mask, is_causal=True)
+        expected_exc = None
     except RuntimeError as exc:
-        expected, expected_exc = None, type(exc)
-    calls = {"n": 0}
+        expected_exc = type(exc)
+    calls = {"n": 0, "out": None}
     with use_rdna3_flash_attention():
         real = sdpa_mod._original_sdpa
 
         def spy(*a, **kw):
             calls["n"] += 1
-            return real(*a, **kw)
+            calls["out"] = real(*a, **kw)
+            return calls["out"]
 
         sdpa_mod._original_sdpa = spy
         try:
@@ -301,8 +303,11 @@ def test_dispatch_defers_causal_with_mask_to_original():
                 with pytest.raises(expected_exc):
                     F.scaled_dot_product_attention(q, q, q, attn_mask=mask, is_causal=True)
             else:
+                # The stock result itself is returned (torch's own values for
+                # this mask + is_causal combination differ from call to call
+                # on some builds, so they are not compared across calls).
                 out = F.scaled_dot_product_attention(q, q, q, attn_mask=mask, is_causal=True)
-                torch.testing.assert_close(out, expected)
+                assert out is calls["out"]
         finally:
             sdpa_mod._original_sdpa = real
     assert calls["n"] == 1
