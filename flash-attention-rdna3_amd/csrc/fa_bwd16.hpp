@@ -452,8 +452,13 @@ struct Dq16Cfg {
   static constexpr int NDB = D / 32;
 };
 
+// flags: bit 0 computes delta in this kernel (fused); bit 1 runs only the
+// (sequence, query head) pairs whose dS region does not fit the scratch
+// (varlen lengths beyond what max_seqlen / total promised): the dQ-from-dS
+// pass skipped those, so this launch gives them the recomputed dQ.
 template <typename Tag, int D, int MODE>
-__global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m_blocks, int fuse_delta) {
+__global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m_blocks, int flags) {
+  const int fuse_delta = flags & 1;
   using C = Dq16Cfg<D>;
   using EL = Elem<Tag>;
   using S = uint16_t;
@@ -481,6 +486,7 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
   }
   const int m0 = mblk * C::BM;
   if (m0 >= sq) return;
+  if ((flags & 2) && ds_region(p, b, hq, sq, sk) >= 0) return;
 
   const S* kbase = reinterpret_cast<const S*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1] +
                    (int64_t)k_start * f.k_stride[2];

@@ -660,6 +660,21 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
         e = launch_dqs16<Tag, D, 1>(p, grid, nmb, dq_scale, stream);
       }
       if (e != hipSuccess) return e;
+      // Varlen: a sequence longer than max_seqlen / total promised has no
+      // room in the scratch; dQ from dS left its heads alone and they get
+      // the recomputed dQ here (the launch exits at once for every other
+      // head).  Dense scratch is sized exactly, so no such head exists.
+      if (f.cu_seqlens_q) {
+        using CQ = Dq16Cfg<D>;
+        auto kq = dq16_kernel<Tag, D, MODE>;
+        e = allow_lds((const void*)kq, CQ::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        const int nq = (f.seqlen_q + CQ::BM - 1) / CQ::BM;
+        const long gq = (long)nq * f.batch * f.heads_q;
+        hipLaunchKernelGGL(kq, dim3((unsigned)gq), dim3(CQ::NT), CQ::LDS_BYTES, stream, p, nq, 2);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+      }
     }
     }
     if ((phases & 4) && !use_ds) {

@@ -107,3 +107,42 @@ def test_varlen_ds_path_matches_recompute(dtype, opts):
     out_a, g_a, out_b, g_b = _both(fn, q, k, v, do)
     assert torch.equal(out_a, out_b)
     _check(g_a, g_b, dtype)
+
+
+@pytest.mark.parametrize("lengths", [[60, 40, 700, 20], [700, 60, 40, 20]])
+def test_varlen_understated_max_seqlen_gets_recomputed_dq(lengths):
+    """max_seqlen below a sequence's real length: the scratch bound (from
+    max_seqlen and total) leaves that sequence's dS no room.  Its heads must
+    get the recomputed dQ (as with no scratch at all), not a skipped one; the
+    rows both paths define (the first max_seqlen of each sequence) agree."""
+    dtype = torch.float16
+    torch.manual_seed(11)
+    total, mx = sum(lengths), 128
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32, device=DEVICE)
+    q, do = _rand((total, 4, 128), dtype), _rand((total, 4, 128), dtype)
+    k, v = _rand((total, 2, 128), dtype), _rand((total, 2, 128), dtype)
+    # (Rows past max_seqlen are left unwritten by the forward; only dQ rows
+    # that both paths define are compared.)
+    def fn(a, b, c):
+        return flash_attention_varlen(a, b, c, cu, cu, mx, mx, causal=True)
+
+    def grads():
+        leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+        out = fn(*leaves)
+        out.backward(do)
+        return leaves[0].grad
+
+    dq_a = grads()
+    saved = _native.set_ds_scratch_limit(0)
+    try:
+        dq_b = grads()
+    finally:
+        _native.set_ds_scratch_limit(saved)
+    start = 0
+    for n in lengths:
+        rows = slice(start, start + min(n, mx))
+        a, b = dq_a[rows].float(), dq_b[rows].float()
+        scale = b.abs().max().item()
+        assert torch.isfinite(a).all() and scale > 0
+        assert (a - b).abs().max().item() <= 4 * 2.0 ** -10 * max(scale, 1e-3), n
+        start += n
