@@ -452,13 +452,10 @@ struct Dq16Cfg {
   static constexpr int NDB = D / 32;
 };
 
-// flags: bit 0 computes delta in this kernel (fused); bit 1 runs only the
-// (sequence, query head) pairs whose dS region does not fit the scratch
-// (varlen lengths beyond what max_seqlen / total promised): the dQ-from-dS
-// pass skipped those, so this launch gives them the recomputed dQ.
+// One 128-row query block (mb_rev counts from the last block) of (sequence,
+// query head) bh; fuse_delta computes delta here.
 template <typename Tag, int D, int MODE>
-__global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m_blocks, int flags) {
-  const int fuse_delta = flags & 1;
+__device__ inline void dq16_block(const fa_bwd_params& p, int num_m_blocks, int mb_rev, int bh, int fuse_delta) {
   using C = Dq16Cfg<D>;
   using EL = Elem<Tag>;
   using S = uint16_t;
@@ -472,9 +469,6 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
   const int wave = wave8 % C::NQ;
   const int htid = tid % C::NTH;
   const int h = lane >> 5, l32 = lane & 31;
-  const int bh_count = f.batch * f.heads_q;
-  const int mb_rev = blockIdx.x / bh_count;
-  const int bh = blockIdx.x - mb_rev * bh_count;
   const int b = bh / f.heads_q, hq = bh - b * f.heads_q;
   const int hk = hq / (f.heads_q / f.heads_kv);
   const int mblk = num_m_blocks - 1 - mb_rev;  // heaviest causal blocks first
@@ -486,7 +480,6 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
   }
   const int m0 = mblk * C::BM;
   if (m0 >= sq) return;
-  if ((flags & 2) && ds_region(p, b, hq, sq, sk) >= 0) return;
 
   const S* kbase = reinterpret_cast<const S*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1] +
                    (int64_t)k_start * f.k_stride[2];
@@ -733,6 +726,34 @@ __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m
     }
 }
 
+
+// flags: bit 0 computes delta in this kernel (fused).  Bit 1 is the
+// fallback pass after dQ from stored dS: one workgroup per (sequence, query
+// head), which returns at once unless that pair's dS region did not fit the
+// scratch (varlen lengths beyond what max_seqlen / total promised); such a
+// pair gets the recomputed dQ of all its query blocks here.
+template <typename Tag, int D, int MODE>
+__global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m_blocks, int flags) {
+  const fa_fwd_params& f = p.fwd;
+  if (flags & 2) {
+    const int bh = blockIdx.x;
+    const int b = bh / f.heads_q, hq = bh - b * f.heads_q;
+    int q_start = 0, sq = f.seqlen_q, k_start = 0, sk = f.seqlen_k;
+    if (f.cu_seqlens_q) {
+      bounded_seq(f.cu_seqlens_q, b, f.total_q, q_start, sq);
+      bounded_seq(f.cu_seqlens_k, b, f.total_k, k_start, sk);
+    }
+    if (ds_region(p, b, hq, sq, sk) >= 0) return;
+    for (int mb_rev = 0; mb_rev < num_m_blocks; ++mb_rev) {
+      dq16_block<Tag, D, MODE>(p, num_m_blocks, mb_rev, bh, 0);
+      __syncthreads();  // every wave is back here; the next block reuses LDS
+    }
+    return;
+  }
+  const int bh_count = f.batch * f.heads_q;
+  const int mb_rev = blockIdx.x / bh_count;
+  dq16_block<Tag, D, MODE>(p, num_m_blocks, mb_rev, blockIdx.x - mb_rev * bh_count, flags & 1);
+}
 
 // ---------------------------------------------------------------------------
 // dQ from stored dS: dQ = scale * dS K.  The dK/dV pass stores the 16-bit dS

@@ -662,15 +662,16 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
       if (e != hipSuccess) return e;
       // Varlen: a sequence longer than max_seqlen / total promised has no
       // room in the scratch; dQ from dS left its heads alone and they get
-      // the recomputed dQ here (the launch exits at once for every other
-      // head).  Dense scratch is sized exactly, so no such head exists.
+      // the recomputed dQ here (one workgroup per sequence and head, which
+      // returns at once when its region fit).  Dense scratch is sized
+      // exactly, so no such head exists.
       if (f.cu_seqlens_q) {
         using CQ = Dq16Cfg<D>;
         auto kq = dq16_kernel<Tag, D, MODE>;
         e = allow_lds((const void*)kq, CQ::LDS_BYTES);
         if (e != hipSuccess) return e;
         const int nq = (f.seqlen_q + CQ::BM - 1) / CQ::BM;
-        const long gq = (long)nq * f.batch * f.heads_q;
+        const long gq = (long)f.batch * f.heads_q;
         hipLaunchKernelGGL(kq, dim3((unsigned)gq), dim3(CQ::NT), CQ::LDS_BYTES, stream, p, nq, 2);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
