@@ -160,9 +160,60 @@ size_t fa_bwd_workspace_bytes(const fa_bwd_params* params) {
   return fa::bwd_ds_bytes(*params);
 }
 
+// With dS scratch, phase 2 alone reads the dS that phase 1 stored there.
+// Each phase-1 launch on a scratch records what it computed (the forward
+// problem, dO, delta and the scratch size); phase 2 alone on that scratch
+// must match the record, or it is refused instead of reading stale dS.
+// (Memory reused by someone else between the two calls cannot be seen.)
+namespace {
+struct DsRecord {
+  fa_fwd_params fwd;
+  const void* dout;
+  int64_t dout_stride[4];
+  const float* delta;
+  int64_t delta_stride[3];
+  int64_t bytes;
+};
+
+std::mutex g_ds_mu;
+std::unordered_map<const void*, DsRecord> g_ds_records;
+
+DsRecord ds_record_of(const fa_bwd_params& p) {
+  DsRecord r;
+  std::memset(&r, 0, sizeof(r));
+  r.fwd = p.fwd;
+  r.dout = p.dout;
+  std::memcpy(r.dout_stride, p.dout_stride, sizeof(r.dout_stride));
+  r.delta = p.delta;
+  std::memcpy(r.delta_stride, p.delta_stride, sizeof(r.delta_stride));
+  r.bytes = p.ds_workspace_bytes;
+  return r;
+}
+
+bool ds_scratch_used(const fa_bwd_params& p) {
+  if (!p.ds_workspace) return false;
+  const size_t need = fa::bwd_ds_bytes(p);
+  return need > 0 && p.ds_workspace_bytes >= (int64_t)need;
+}
+}  // namespace
+
 int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream) {
   if (phase < 0 || phase > 2) return fail(FA_ERR_INVALID, "fa_bwd_phase: phase %d not in 0..2", phase);
-  return bwd_common(params, 1 << phase, stream);
+  if (params && phase == 2 && ds_scratch_used(*params)) {
+    const DsRecord want = ds_record_of(*params);
+    std::lock_guard<std::mutex> lock(g_ds_mu);
+    const auto it = g_ds_records.find(params->ds_workspace);
+    if (it == g_ds_records.end() || std::memcmp(&it->second, &want, sizeof(want)) != 0)
+      return fail(FA_ERR_INVALID,
+                  "fa_bwd_phase: phase 2 with ds_workspace reads the dS that phase 1 of the same problem "
+                  "stores there; run phase 1 on this scratch first (or pass no ds_workspace to recompute dQ)");
+  }
+  const int rc = bwd_common(params, 1 << phase, stream);
+  if (rc == FA_OK && phase == 1 && ds_scratch_used(*params)) {
+    std::lock_guard<std::mutex> lock(g_ds_mu);
+    g_ds_records[params->ds_workspace] = ds_record_of(*params);
+  }
+  return rc;
 }
 
 namespace {

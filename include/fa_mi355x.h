@@ -315,7 +315,11 @@ int fa_bwd(const fa_bwd_params* params, void* stream);
 /* One stage of fa_bwd: 0 = delta, 1 = dK/dV, 2 = dQ (1 and 2 read delta).
  * No counterpart in the reference (its three backward launches are separate
  * Triton calls, interface.py:226/:236/:258); it exists so profilers and
- * benchmarks can time each backward kernel on its own. */
+ * benchmarks can time each backward kernel on its own.  With ds_workspace,
+ * phase 2 reads the dS that phase 1 stored there: phase 2 is refused
+ * (FA_ERR_INVALID) unless the last phase-1 call on that scratch had the same
+ * forward problem, dout, delta and scratch size (memory reused by others in
+ * between cannot be detected). */
 int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream);
 /* Bytes of ds_workspace the backward of `params` can use (0: the dS path
  * does not apply: fp32, head_dim other than 64 or 128, or more than 512

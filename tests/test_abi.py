@@ -130,3 +130,29 @@ def test_torch_host_operators_refuse_host_tensors():
             fn(q, q, q, *args)
     with pytest.raises(Exception, match="GPU|CUDA|backend"):
         ops.backward(q, q, q, q, q, torch.zeros(1, 1, 8), *args)
+
+
+def test_bwd_phase2_on_unfilled_ds_scratch_is_refused():
+    """With dS scratch, dQ alone (fa_bwd_phase 2) reads the dS that phase 1
+    stored; on a scratch where phase 1 of that problem never ran it is
+    refused before any launch (no GPU needed for the refusal)."""
+    lib = _native.lib()
+    p = _native.BwdParams()
+    f = p.fwd
+    f.abi_version, f.dtype = _native.ABI_VERSION, 0
+    f.batch, f.heads_q, f.heads_kv, f.seqlen_q, f.seqlen_k, f.head_dim = 1, 2, 2, 256, 256, 128
+    f.softmax_scale = 0.125
+    base = 1 << 32
+    f.q, f.k, f.v, f.out, f.lse = base, base + (1 << 24), base + (2 << 24), base + (3 << 24), base + (4 << 24)
+    p.dout, p.dq, p.dk, p.dv, p.delta = (base + (i << 24) for i in range(5, 10))
+    for name in ("q_stride", "k_stride", "v_stride", "out_stride"):
+        getattr(f, name)[:] = [2 * 256 * 128, 256 * 128, 128, 1]
+    for name in ("dout_stride", "dq_stride", "dk_stride", "dv_stride"):
+        getattr(p, name)[:] = [2 * 256 * 128, 256 * 128, 128, 1]
+    f.lse_stride[:] = [512, 256, 1]
+    p.delta_stride[:] = [512, 256, 1]
+    need = lib.fa_bwd_workspace_bytes(ctypes.byref(p))
+    assert need > 0
+    p.ds_workspace, p.ds_workspace_bytes = base + (12 << 24), need
+    assert lib.fa_bwd_phase(ctypes.byref(p), 2, None) == 1
+    assert b"phase 1" in lib.fa_last_error_string()

@@ -146,3 +146,24 @@ def test_varlen_understated_max_seqlen_gets_recomputed_dq(lengths):
         assert torch.isfinite(a).all() and scale > 0
         assert (a - b).abs().max().item() <= 4 * 2.0 ** -10 * max(scale, 1e-3), n
         start += n
+
+
+def test_phase_api_dq_needs_its_dkdv_phase_first():
+    """The per-kernel entry point (fa_bwd_phase): dQ from dS alone is refused
+    until phase 1 of the same problem has filled the scratch, then matches
+    the full backward's dQ bit for bit."""
+    from fa_rdna3.interface import _backward, _backward_launcher, _forward
+
+    torch.manual_seed(3)
+    q, k, v, do = (_rand((1, 4, 300, 128), torch.float16) for _ in range(4))
+    scale = 128 ** -0.5
+    out, lse = _forward(q, k, v, True, scale, (-1, -1), 0.0, None, None, 0.0, 0)
+    launch = _backward_launcher(do, q, k, v, out, lse, True, scale, (-1, -1), 0.0, None, None, 0.0, 0)
+    launch(0)
+    with pytest.raises(RuntimeError, match="phase 1"):
+        launch(2)
+    launch(1)
+    dq, dk, dv, _ = launch(2)
+    ref = _backward(do, q, k, v, out, lse, True, scale, (-1, -1), 0.0, None, None, 0.0, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(dq, ref[0]) and torch.equal(dk, ref[1]) and torch.equal(dv, ref[2])
