@@ -156,3 +156,15 @@ def test_bwd_phase2_on_unfilled_ds_scratch_is_refused():
     p.ds_workspace, p.ds_workspace_bytes = base + (12 << 24), need
     assert lib.fa_bwd_phase(ctypes.byref(p), 2, None) == 1
     assert b"phase 1" in lib.fa_last_error_string()
+
+
+def test_hbm_read_probe_describes_its_variants_and_checks_arguments():
+    """The read-ceiling probe exports a variant list and rejects bad
+    arguments before any launch (no GPU needed for either)."""
+    lib = _native.lib()
+    names = _native.hbm_read_probe_variants()
+    assert len(names) == lib.fa_hbm_read_probe_count() >= 12
+    assert all("threads" in n for n in names)
+    assert lib.fa_hbm_read_probe(None, 256, None, 0, None) == 1
+    assert lib.fa_hbm_read_probe(1 << 32, 24, 1 << 33, 0, None) == 1   # size not a multiple of 16
+    assert lib.fa_hbm_read_probe(1 << 32, 256, 1 << 33, -1, None) == 1
