@@ -805,8 +805,8 @@ struct Dqs16Cfg {
 // One work item (query block `item / (B * Hq)` from the heavy end of
 // (batch, head) `item % (B * Hq)`); `end_barrier` as in fwd16_item.
 template <typename Tag, int D, int OCC>
-__device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blocks, float dq_scale, int item,
-                                           unsigned char* smem_raw, bool end_barrier) {
+__device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blocks, float dq_scale, bool ds_nt,
+                                           int item, unsigned char* smem_raw, bool end_barrier) {
   using C = Dqs16Cfg<D, OCC>;
   using EL = Elem<Tag>;
   using S = uint16_t;
@@ -889,7 +889,9 @@ __device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blo
     // zeroed by the visibility mask of the partly visible step).
     const int r0 = n0 % kDsTileKeys;  // first key row of the step within the tile
     const S* dtile = dsbase + (int64_t)(n0 / kDsTileKeys) * qblocks * kDsTileElems + r0 * kDsSubQueries;
-    sd.load(rsrc_words(dtile, (kDsTileElems - r0 * kDsSubQueries) * 2), base + C::KT * 2u, wave);
+    const i32x4 drs = rsrc_words(dtile, (kDsTileElems - r0 * kDsSubQueries) * 2);
+    if (ds_nt) sd.load_nt(drs, base + C::KT * 2u, wave);
+    else sd.load(drs, base + C::KT * 2u, wave);
   };
 
   // Visible keys of this lane's row: partly visible tiles zero the dS of
@@ -963,18 +965,20 @@ __device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blo
 
 // PAIR: workgroup (j, b·Hq) runs query block j from the heavy end, then
 // from the light end, of the same (batch, head), like fwd16_kernel.
+// ds_nt: read dS with nontemporal loads (scratch too large for the 256 MiB
+// memory-side cache, so the dS lines only displace reused K rows from L2).
 template <typename Tag, int D, int OCC, bool PAIR>
-__global__ __launch_bounds__(512, OCC) void dqs16_kernel(fa_bwd_params p, int num_m_blocks, float dq_scale) {
+__global__ __launch_bounds__(512, OCC) void dqs16_kernel(fa_bwd_params p, int num_m_blocks, float dq_scale, int ds_nt) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   if constexpr (!PAIR) {
-    dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, blockIdx.x, smem_raw, false);
+    dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, ds_nt != 0, blockIdx.x, smem_raw, false);
   } else {
     const int bh_count = p.fwd.batch * p.fwd.heads_q;
     const int j = blockIdx.x / bh_count;
     const int bh = blockIdx.x - j * bh_count;
     const int j2 = num_m_blocks - 1 - j;
-    dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, j * bh_count + bh, smem_raw, j2 != j);
-    if (j2 != j) dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, j2 * bh_count + bh, smem_raw, false);
+    dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, ds_nt != 0, j * bh_count + bh, smem_raw, j2 != j);
+    if (j2 != j) dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, ds_nt != 0, j2 * bh_count + bh, smem_raw, false);
   }
 }
 

@@ -597,12 +597,13 @@ static hipError_t run_bwd_dkdv16(const fa_bwd_params& p, hipStream_t stream) {
 }
 
 template <typename Tag, int D, int OCC, bool PAIR = false>
-static hipError_t launch_dqs16(const fa_bwd_params& p, long grid, int nmb, float dq_scale, hipStream_t stream) {
+static hipError_t launch_dqs16(const fa_bwd_params& p, long grid, int nmb, float dq_scale, int ds_nt,
+                               hipStream_t stream) {
   using C = Dqs16Cfg<D, OCC>;
   auto kern = dqs16_kernel<Tag, D, OCC, PAIR>;
   hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb, dq_scale);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb, dq_scale, ds_nt);
   return hipGetLastError();
 }
 
@@ -645,6 +646,12 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
       const long grid = (long)nmb * f.batch * f.heads_q;
       // MODE 3 stores dS / 4 (its softcap factor is (1 - tanh^2) / 4).
       const float dq_scale = f.softmax_scale * (MODE == 3 ? 4.f : 1.f);
+      // A scratch bound above twice the 256 MiB memory-side cache: the dS
+      // comes from HBM either way, and nontemporal loads keep it out of L2
+      // (config 5, 3.0 GB bound: dQ 303.5 -> 295.2 us).  Below it the plain
+      // loads hit the dS the dK/dV pass left in that cache (config 2, 268 MB
+      // bound: 36 against 39 us with nontemporal loads).
+      const int ds_nt = bwd_ds_bytes(p) > (size_t(512) << 20) ? 1 : 0;
       // Two workgroups per CU (D = 128) once the launch spans more than
       // three rounds of one workgroup per CU; below that, heavy and light
       // query blocks of a head paired in one workgroup when the pairs still
@@ -653,11 +660,11 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
       if constexpr (D >= 128) {
         const long cus = device_cu_count();
         const long pairs = (long)((nmb + 1) / 2) * f.batch * f.heads_q;
-        if (grid > 3L * cus) e = launch_dqs16<Tag, D, 2>(p, grid, nmb, dq_scale, stream);
-        else if (pairs >= cus) e = launch_dqs16<Tag, D, 1, true>(p, pairs, nmb, dq_scale, stream);
-        else e = launch_dqs16<Tag, D, 1>(p, grid, nmb, dq_scale, stream);
+        if (grid > 3L * cus) e = launch_dqs16<Tag, D, 2>(p, grid, nmb, dq_scale, ds_nt, stream);
+        else if (pairs >= cus) e = launch_dqs16<Tag, D, 1, true>(p, pairs, nmb, dq_scale, ds_nt, stream);
+        else e = launch_dqs16<Tag, D, 1>(p, grid, nmb, dq_scale, ds_nt, stream);
       } else {
-        e = launch_dqs16<Tag, D, 1>(p, grid, nmb, dq_scale, stream);
+        e = launch_dqs16<Tag, D, 1>(p, grid, nmb, dq_scale, ds_nt, stream);
       }
       if (e != hipSuccess) return e;
       // Varlen: a sequence longer than max_seqlen / total promised has no

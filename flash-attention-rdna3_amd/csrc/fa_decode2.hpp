@@ -2,12 +2,12 @@
 // paged cache.  Same results as decode_kernel (reference kernels/decode.py:9-125,
 // kernels/paged.py:16-89); organised for HBM throughput on gfx950:
 //
-//  * K rows load straight into registers in the MFMA operand layout; V bytes
-//    go HBM -> LDS with global_load_lds_dwordx4 (each lane picks the source
-//    of its 16-byte LDS slot, which both gathers paged rows and applies the
-//    XOR swizzle of the LDS tile).
+//  * K rows load straight into registers in the MFMA operand layout; V rows
+//    load into registers as raw 16-byte pieces (each instruction reads four
+//    whole 256-byte rows) and go to a per-wave swizzled LDS tile just before
+//    use, from which the P.V MFMA reads them transposed.
 //  * Every wave streams its own 32-key chunks through NBUF private slots
-//    (up to 64 KB in flight per wave) and synchronises only with itself
+//    (128 VGPRs of slots: 32 KiB in flight per wave) and synchronises only with itself
 //    (s_waitcnt), so the workgroup never stalls on a barrier in the key loop.
 //  * Scores use v_mfma_f32_16x16x32: the packed GQA rows (group heads x Sq,
 //    usually 4) occupy 16 MFMA columns instead of 32.  P^T feeds the P.V MFMA

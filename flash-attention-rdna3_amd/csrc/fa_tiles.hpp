@@ -341,6 +341,14 @@ __device__ inline void buf_load_lds16(i32x4 rs, uint32_t voff, uint32_t lds_addr
                : "memory", "m0");
 }
 
+// The same load, nontemporal: the lines are not kept in L2 for reuse.
+__device__ inline void buf_load_lds16_nt(i32x4 rs, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds"
+               :
+               : "v"(voff), "s"(rs), "s"(lds_addr)
+               : "memory", "m0");
+}
+
 template <int R, int COLS, int NT>
 struct DmaSwzTile {
   static constexpr int CPR = COLS / 8;
@@ -375,6 +383,10 @@ struct DmaSwzTile {
   __device__ inline void load(i32x4 rs, uint32_t lds_tile, int wave) const {
 #pragma unroll
     for (int j = 0; j < PT; ++j) buf_load_lds16(rs, voff[j], lds_tile + (uint32_t)(NT * j + 64 * wave) * 16u);
+  }
+  __device__ inline void load_nt(i32x4 rs, uint32_t lds_tile, int wave) const {
+#pragma unroll
+    for (int j = 0; j < PT; ++j) buf_load_lds16_nt(rs, voff[j], lds_tile + (uint32_t)(NT * j + 64 * wave) * 16u);
   }
 };
 
