@@ -22,6 +22,8 @@
 //  * the 4 wave states (max, sum, O^T) are merged in LDS at the end, so one
 //    partial per workgroup reaches HBM.  With a single split the merged row
 //    is written straight to `out` and no combine kernel runs.
+#include <hip/hip_ext.h>
+
 #include <mutex>
 
 #include "fa_internal.hpp"
@@ -325,6 +327,12 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
   }
 }
 
+// When set, the launch that ends a decode call completes this event (the
+// kernel's own completion signal, no extra queue packet) and clears it; a
+// call whose last launch does not take it leaves it set for the caller to
+// record.  Used by fa_decode_splitk_noalloc to order its calls.
+static thread_local hipEvent_t t_stop_event = nullptr;
+
 template <typename Tag, int D, bool PAGED>
 static hipError_t run_decode(DecodeArgs a, hipStream_t stream) {
   // Paged caches with blocks under 4 keys take the generic kernel (a chunk
@@ -350,7 +358,13 @@ static hipError_t run_decode(DecodeArgs a, hipStream_t stream) {
         auto kern = decode2_kernel<Tag, D, PG, K8>;
         hipError_t err = allow_lds((const void*)kern, C::LDS_BYTES);
         if (err != hipSuccess) return err;
-        hipLaunchKernelGGL(kern, grid, dim3(C::NT), C::LDS_BYTES, stream, a);
+        // With the merge in this launch (tickets), it is the call's last.
+        if (t_stop_event && a.tickets) {
+          hipExtLaunchKernelGGL(kern, grid, dim3(C::NT), C::LDS_BYTES, stream, nullptr, t_stop_event, 0u, a);
+          t_stop_event = nullptr;
+        } else {
+          hipLaunchKernelGGL(kern, grid, dim3(C::NT), C::LDS_BYTES, stream, a);
+        }
         return hipGetLastError();
       };
       using P1 = std::integral_constant<int, PG1>;
@@ -464,14 +478,63 @@ hipError_t scratch_for_current_device(unsigned char** out) {
 }
 }  // namespace
 
+// Calls on one device are ordered by the order they are made on the host:
+// each call records `done` on its stream, and a call on another stream first
+// waits for the previous call's `done`.  So two streams (or host threads)
+// no longer race on the shared scratch; the mutex keeps the record and the
+// launch of one call together.  Under graph capture there is no wait or
+// record (a captured wait on an event from outside the capture is an error):
+// replays of a captured call must not overlap other calls on that device.
+namespace {
+struct NoallocOrder {
+  hipStream_t last = nullptr;
+  hipEvent_t done = nullptr;  // created on the device's first call outside capture
+};
+std::mutex g_order_mu;
+NoallocOrder g_order[kMaxDevices];
+}  // namespace
+
 hipError_t launch_decode_noalloc(const fa_decode_params& p, hipStream_t s) {
   unsigned char* base = nullptr;
   hipError_t e = scratch_for_current_device(&base);
   if (e != hipSuccess) return e;
+  int dev = 0;
+  e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(s, &cs);
+  if (e != hipSuccess) return e;
+  const bool capturing = cs != hipStreamCaptureStatusNone;
   fa_decode_params q = p;
   q.tickets = reinterpret_cast<uint32_t*>(base);
   q.workspace = base + kNoallocTicketBytes;
-  return launch_decode(q, s);
+  std::lock_guard<std::mutex> lock(g_order_mu);
+  NoallocOrder& o = g_order[dev];
+  if (!capturing && o.done && o.last != s) {
+    e = hipStreamWaitEvent(s, o.done, 0);
+    if (e != hipSuccess) return e;
+  }
+  if (capturing) return launch_decode(q, s);
+  if (!o.done) {
+    e = hipEventCreateWithFlags(&o.done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      o.done = nullptr;
+      return e;
+    }
+  }
+  // The single-launch path completes `done` with its kernel; the others
+  // leave t_stop_event set and `done` is recorded after them.
+  t_stop_event = o.done;
+  e = launch_decode(q, s);
+  const bool taken = t_stop_event == nullptr;
+  t_stop_event = nullptr;
+  if (e != hipSuccess) return e;
+  if (!taken) {
+    e = hipEventRecord(o.done, s);
+    if (e != hipSuccess) return e;
+  }
+  o.last = s;
+  return hipSuccess;
 }
 
 hipError_t launch_paged(const fa_paged_params& p, hipStream_t s) {

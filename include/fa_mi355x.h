@@ -344,10 +344,13 @@ int fa_decode_splitk(const fa_decode_params* params, void* stream);
  * bytes, one per GPU, held until the process ends.  A call that would need
  * more (fa_decode_workspace_bytes(...) > FA_NOALLOC_WORKSPACE_BYTES, or
  * batch * heads_q * seqlen_q > FA_NOALLOC_TICKETS) fails with FA_ERR_INVALID.
- * Every call on one GPU shares that GPU's scratch: calls that overlap in time
- * on one GPU (different streams, or host threads) race and must be
- * serialised by the caller.  The counters start at zero when the library
- * loads and every call leaves them at zero.
+ * Every call on one GPU shares that GPU's scratch.  Calls made outside graph
+ * capture are ordered on the device in the order they are made on the host:
+ * a call on another stream than the previous call's first waits for that
+ * call (an event the library creates on the device's first call, completed
+ * by the decode kernel itself; no device memory).  Under graph capture nothing is recorded or waited for, so graph
+ * replays must not overlap other calls on the same GPU.  The counters start
+ * at zero when the library loads and every call leaves them at zero.
  */
 #define FA_NOALLOC_WORKSPACE_BYTES (32 * 1024 * 1024)
 #define FA_NOALLOC_TICKETS 65536

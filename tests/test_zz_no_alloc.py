@@ -113,3 +113,44 @@ def test_noalloc_replays_under_hip_graph_capture():
         torch.cuda.synchronize()
         torch.testing.assert_close(out, eager, atol=0, rtol=0)
         _ = (k[:, :, :64].float() * (i + 1)).sum().item()  # eager work between replays
+
+
+def test_noalloc_calls_on_two_streams_are_ordered():
+    # Calls on different streams share the static scratch; the entry point
+    # orders each call after the previous one on the device (an event wait),
+    # so back-to-back calls on two streams without any caller
+    # synchronisation both give the allocating entry point's bits.
+    g = torch.Generator().manual_seed(11)
+    cases = []
+    for i, (b, sk) in enumerate(((4, 8192), (2, 3000), (4, 6000), (1, 8192), (3, 2048), (4, 8192))):
+        q = torch.randn(b, 32, 1, 128, generator=g).half().to(DEVICE)
+        k = torch.randn(b, 8, sk, 128, generator=g).half().to(DEVICE)
+        v = torch.randn(b, 8, sk, 128, generator=g).half().to(DEVICE)
+        lens = torch.randint(1, sk + 1, (b,), generator=g).to(torch.int32).to(DEVICE)
+        splits = 8
+        ref = torch.empty_like(q)
+        ws = torch.empty(_native.decode_workspace_bytes(b, 32, 1, 128, splits), dtype=torch.uint8, device=DEVICE)
+        tickets = torch.zeros(b * 32, dtype=torch.int32, device=DEVICE)
+        p = _params(q, k, v, ref, lens, splits)
+        p.workspace, p.tickets = ws.data_ptr(), tickets.data_ptr()
+        assert _call("fa_decode_splitk", p)[0] == 0
+        out = torch.full_like(q, float("nan"))
+        # The params hold raw pointers: keep the tensors alive with them.
+        cases.append((_params(q, k, v, out, lens, splits), out, ref, (q, k, v, lens)))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    # A long matrix product ahead of the first call keeps stream 0 busy, so
+    # the calls queued behind it on both streams would otherwise overlap.
+    big = torch.randn(4096, 4096, device=DEVICE, dtype=torch.float16)
+    with torch.cuda.stream(streams[0]):
+        for _ in range(4):
+            big = big @ big
+            big = big / big.abs().amax().clamp(min=1)
+    for i, (p, out, _, _) in enumerate(cases):
+        with torch.cuda.stream(streams[i % 2]):
+            rc, msg = _call("fa_decode_splitk_noalloc", p)
+        assert rc == 0, msg
+    torch.cuda.synchronize()
+    print("noalloc two streams: 6 calls", flush=True)
+    for p, out, ref, _ in cases:
+        torch.testing.assert_close(out, ref, atol=0, rtol=0)
