@@ -447,6 +447,39 @@ def run_cfg5(iters=20):
     return {"ms": round(dt * 1e3, 3), "TFLOP/s": round((fwd + bwd) / dt / 1e12, 1)}
 
 
+def run_varlen_many(iters=20):
+    """Many short packed sequences: 400 of 64-192 tokens (seed 3), Hq=32,
+    Hkv=8, D=128 fp16 causal fwd + bwd, warmed up, then `iters` steps; GFLOP
+    by the cfg2 convention (fwd 4*D*Hq*pairs, fwd + bwd 3.5x that)."""
+    from fa_rdna3 import flash_attention_varlen
+
+    g = torch.Generator().manual_seed(3)
+    lengths = torch.randint(64, 193, (400,), generator=g).tolist()
+    total = sum(lengths)
+    q, do = (torch.randn(total, 32, 128, generator=g).half().cuda() for _ in range(2))
+    k, v = (torch.randn(total, 8, 128, generator=g).half().cuda() for _ in range(2))
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32).cuda()
+    mx = max(lengths)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        flash_attention_varlen(q, k, v, cu, cu, mx, mx, causal=True).backward(do)
+
+    for _ in range(5):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / iters
+    fwd = 4.0 * 32 * 128 * sum(n * (n + 1) // 2 for n in lengths)
+    return {"ms": round(dt * 1e3, 3), "TFLOP/s": round(3.5 * fwd / dt / 1e12, 1),
+            "shape": "400 sequences of 64-192 tokens, Hq=32 Hkv=8 D=128 fp16 causal fwd+bwd"}
+
+
 def run_long_causal(iters=5):
     """A long causal sequence: B=1, H=32, S=16384, D=128 fp16 fwd + bwd
     (7.70 TFLOP by the cfg2 convention), warmed up, then `iters` steps."""
@@ -835,6 +868,7 @@ def main():
         line["decode"] = run_decode_configs()
         line["cfg5_varlen"] = run_cfg5()
         line["long_causal"] = run_long_causal()
+        line["varlen_many"] = run_varlen_many()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
         line["cpu_baseline_configs"] = cpu_baseline_configs()

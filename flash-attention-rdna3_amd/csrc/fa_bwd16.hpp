@@ -22,24 +22,39 @@ namespace fa {
 
 __device__ inline float lse2_of(float lse) { return lse == kNegInf ? __builtin_inff() : lse * kLog2e; }
 
-// Start (elements) of the dS region of (sequence b, query head hq) in the
-// scratch, or -1 when it would not fit (varlen lengths inconsistent with
-// max_seqlen / total): then nothing is stored there or read from it.
-__device__ inline int64_t ds_region(const fa_bwd_params& p, int b, int hq, int sq, int sk) {
+// Elements of the dS scratch before sequence b's regions.  WAVE: called by
+// a whole wave (every lane active); for varlen, lane i then sums the regions
+// of sequences i, i + 64, ... below b (one round trip per 64 sequences) and a
+// wave reduction adds the lanes; otherwise one thread walks them in turn.
+// (A batch of 400 sequences: walking them one by one took the dK/dV pass
+// 3.36 ms and dQ 1.88 ms, against 0.61 and 0.37 ms with the wave sum.)
+template <bool WAVE>
+__device__ inline int64_t ds_seq_base(const fa_bwd_params& p, int b, int sq, int sk) {
   const fa_fwd_params& f = p.fwd;
-  int64_t base;
-  if (!f.cu_seqlens_q) {
-    base = (int64_t)b * f.heads_q * ds_region_elems(sq, sk);
-  } else {
-    int64_t acc = 0;
-    for (int i = 0; i < b; ++i) {
+  if (!f.cu_seqlens_q) return (int64_t)b * f.heads_q * ds_region_elems(sq, sk);
+  const int lane = WAVE ? (int)(threadIdx.x & 63) : 0;
+  const int step = WAVE ? 64 : 1;
+  int64_t acc = 0;
+  for (int i = lane; i - lane < b; i += step) {
+    if (i < b) {
       int s0, l0, s1, l1;
       bounded_seq(f.cu_seqlens_q, i, f.total_q, s0, l0);
       bounded_seq(f.cu_seqlens_k, i, f.total_k, s1, l1);
       acc += ds_region_elems(l0, l1);
     }
-    base = acc * f.heads_q;
   }
+  if constexpr (WAVE) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  }
+  return acc * f.heads_q;
+}
+
+// Start (elements) of the dS region of query head hq of a sequence whose
+// regions start at `base`, or -1 when it would not fit (varlen lengths
+// inconsistent with max_seqlen / total): then nothing is stored there or
+// read from it.
+__device__ inline int64_t ds_region_at(const fa_bwd_params& p, int64_t base, int hq, int sq, int sk) {
   const int64_t start = base + (int64_t)hq * ds_region_elems(sq, sk);
   const int64_t cap = (p.ds_workspace_bytes - 1024) / 2;
   return (start + ds_region_elems(sq, sk) <= cap) ? start : -1;
@@ -151,6 +166,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
   const uint32_t lds0 = lds_addr(hsmem);
   const int nlast = min(n0 + C::BN, sk) - 1;
 
+  const int64_t ds_base = p.ds_workspace != nullptr ? ds_seq_base<true>(p, b, sq, sk) : 0;
   for (int g = 0; g < group; ++g) {
     const int hq = hk * group + g;
     const Mods md = make_mods(f, b, hq, sq, sk);
@@ -222,7 +238,7 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
     S* dsn = nullptr;
     S* ds_dump = nullptr;
     if (p.ds_workspace != nullptr) {
-      const int64_t region = ds_region(p, b, hq, sq, sk);
+      const int64_t region = ds_region_at(p, ds_base, hq, sq, sk);
       ds_on = region >= 0;
       S* const ws = reinterpret_cast<S*>(p.ds_workspace);
       // row n % 64 of the key block's tiles; + (query block) * tile
@@ -728,25 +744,29 @@ __device__ inline void dq16_block(const fa_bwd_params& p, int num_m_blocks, int 
 
 
 // flags: bit 0 computes delta in this kernel (fused).  Bit 1 is the
-// fallback pass after dQ from stored dS: one workgroup per (sequence, query
-// head), which returns at once unless that pair's dS region did not fit the
-// scratch (varlen lengths beyond what max_seqlen / total promised); such a
-// pair gets the recomputed dQ of all its query blocks here.
+// fallback pass after dQ from stored dS: one workgroup per sequence, which
+// returns at once unless some head's dS region did not fit the scratch
+// (varlen lengths beyond what max_seqlen / total promised; a region's end
+// grows with the head index, so the last head decides); the heads that did
+// not fit get the recomputed dQ of all their query blocks here.
 template <typename Tag, int D, int MODE>
 __global__ __launch_bounds__(512, 1) void dq16_kernel(fa_bwd_params p, int num_m_blocks, int flags) {
   const fa_fwd_params& f = p.fwd;
   if (flags & 2) {
-    const int bh = blockIdx.x;
-    const int b = bh / f.heads_q, hq = bh - b * f.heads_q;
+    const int b = blockIdx.x;
     int q_start = 0, sq = f.seqlen_q, k_start = 0, sk = f.seqlen_k;
     if (f.cu_seqlens_q) {
       bounded_seq(f.cu_seqlens_q, b, f.total_q, q_start, sq);
       bounded_seq(f.cu_seqlens_k, b, f.total_k, k_start, sk);
     }
-    if (ds_region(p, b, hq, sq, sk) >= 0) return;
-    for (int mb_rev = 0; mb_rev < num_m_blocks; ++mb_rev) {
-      dq16_block<Tag, D, MODE>(p, num_m_blocks, mb_rev, bh, 0);
-      __syncthreads();  // every wave is back here; the next block reuses LDS
+    const int64_t base = ds_seq_base<true>(p, b, sq, sk);
+    if (ds_region_at(p, base, f.heads_q - 1, sq, sk) >= 0) return;
+    for (int hq = 0; hq < f.heads_q; ++hq) {
+      if (ds_region_at(p, base, hq, sq, sk) >= 0) continue;
+      for (int mb_rev = 0; mb_rev < num_m_blocks; ++mb_rev) {
+        dq16_block<Tag, D, MODE>(p, num_m_blocks, mb_rev, b * f.heads_q + hq, 0);
+        __syncthreads();  // every wave is back here; the next block reuses LDS
+      }
     }
     return;
   }
@@ -804,7 +824,7 @@ struct Dqs16Cfg {
 
 // One work item (query block `item / (B * Hq)` from the heavy end of
 // (batch, head) `item % (B * Hq)`); `end_barrier` as in fwd16_item.
-template <typename Tag, int D, int OCC>
+template <typename Tag, int D, int OCC, bool VARLEN>
 __device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blocks, float dq_scale, bool ds_nt,
                                            int item, unsigned char* smem_raw, bool end_barrier) {
   using C = Dqs16Cfg<D, OCC>;
@@ -827,13 +847,16 @@ __device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blo
   const int mblk = num_m_blocks - 1 - mb_rev;  // heaviest causal blocks first
 
   int q_start = 0, sq = f.seqlen_q, k_start = 0, sk = f.seqlen_k;
-  if (f.cu_seqlens_q) {
+  if constexpr (VARLEN) {
     bounded_seq(f.cu_seqlens_q, b, f.total_q, q_start, sq);
     bounded_seq(f.cu_seqlens_k, b, f.total_k, k_start, sk);
   }
   const int m0 = mblk * C::BM;
   if (m0 >= sq) return;
-  const int64_t region = ds_region(p, b, hq, sq, sk);
+  // The dense form is a separate instantiation without the wave sum:
+  // compiled in, it cost config 2's dQ 3-4 us.
+  const int64_t base = VARLEN ? ds_seq_base<true>(p, b, sq, sk) : (int64_t)b * f.heads_q * ds_region_elems(sq, sk);
+  const int64_t region = ds_region_at(p, base, hq, sq, sk);
   const int64_t qblocks = ds_qblocks(sq);
 
   const S* kbase = reinterpret_cast<const S*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1] +
@@ -967,18 +990,19 @@ __device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blo
 // from the light end, of the same (batch, head), like fwd16_kernel.
 // ds_nt: read dS with nontemporal loads (scratch too large for the 256 MiB
 // memory-side cache, so the dS lines only displace reused K rows from L2).
-template <typename Tag, int D, int OCC, bool PAIR>
+// VARLEN: cu_seqlens_q / cu_seqlens_k are set (the host picks the form).
+template <typename Tag, int D, int OCC, bool PAIR, bool VARLEN>
 __global__ __launch_bounds__(512, OCC) void dqs16_kernel(fa_bwd_params p, int num_m_blocks, float dq_scale, int ds_nt) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   if constexpr (!PAIR) {
-    dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, ds_nt != 0, blockIdx.x, smem_raw, false);
+    dqs16_item<Tag, D, OCC, VARLEN>(p, num_m_blocks, dq_scale, ds_nt != 0, blockIdx.x, smem_raw, false);
   } else {
     const int bh_count = p.fwd.batch * p.fwd.heads_q;
     const int j = blockIdx.x / bh_count;
     const int bh = blockIdx.x - j * bh_count;
     const int j2 = num_m_blocks - 1 - j;
-    dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, ds_nt != 0, j * bh_count + bh, smem_raw, j2 != j);
-    if (j2 != j) dqs16_item<Tag, D, OCC>(p, num_m_blocks, dq_scale, ds_nt != 0, j2 * bh_count + bh, smem_raw, false);
+    dqs16_item<Tag, D, OCC, VARLEN>(p, num_m_blocks, dq_scale, ds_nt != 0, j * bh_count + bh, smem_raw, j2 != j);
+    if (j2 != j) dqs16_item<Tag, D, OCC, VARLEN>(p, num_m_blocks, dq_scale, ds_nt != 0, j2 * bh_count + bh, smem_raw, false);
   }
 }
 

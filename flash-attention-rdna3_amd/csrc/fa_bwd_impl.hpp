@@ -609,11 +609,11 @@ static hipError_t run_bwd_dkdv16(const fa_bwd_params& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <typename Tag, int D, int OCC, bool PAIR = false>
+template <typename Tag, int D, int OCC, bool PAIR = false, bool VARLEN = false>
 static hipError_t launch_dqs16(const fa_bwd_params& p, long grid, int nmb, float dq_scale, int ds_nt,
                                hipStream_t stream) {
   using C = Dqs16Cfg<D, OCC>;
-  auto kern = dqs16_kernel<Tag, D, OCC, PAIR>;
+  auto kern = dqs16_kernel<Tag, D, OCC, PAIR, VARLEN>;
   hipError_t e = allow_lds((const void*)kern, C::LDS_BYTES);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, stream, p, nmb, dq_scale, ds_nt);
@@ -672,30 +672,30 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
       // three rounds of one workgroup per CU; below that, heavy and light
       // query blocks of a head paired in one workgroup when the pairs still
       // give every CU one (config 2: dQ 37.8 -> 36.9 us, same results).
-      hipError_t e;
-      if constexpr (D >= 128) {
-        const long cus = device_cu_count();
-        const long pairs = (long)((nmb + 1) / 2) * f.batch * f.heads_q;
-        if (grid > 3L * cus) e = launch_dqs16<Tag, D, 2>(p, grid, nmb, dq_scale, ds_nt, stream);
-        else if (pairs >= cus) e = launch_dqs16<Tag, D, 1, true>(p, pairs, nmb, dq_scale, ds_nt, stream);
-        else e = launch_dqs16<Tag, D, 1>(p, grid, nmb, dq_scale, ds_nt, stream);
-      } else {
-        e = launch_dqs16<Tag, D, 1>(p, grid, nmb, dq_scale, ds_nt, stream);
-      }
+      auto launch_all = [&](auto varlen_t) -> hipError_t {
+        constexpr bool VL = decltype(varlen_t)::value;
+        if constexpr (D >= 128) {
+          const long cus = device_cu_count();
+          const long pairs = (long)((nmb + 1) / 2) * f.batch * f.heads_q;
+          if (grid > 3L * cus) return launch_dqs16<Tag, D, 2, false, VL>(p, grid, nmb, dq_scale, ds_nt, stream);
+          if (pairs >= cus) return launch_dqs16<Tag, D, 1, true, VL>(p, pairs, nmb, dq_scale, ds_nt, stream);
+        }
+        return launch_dqs16<Tag, D, 1, false, VL>(p, grid, nmb, dq_scale, ds_nt, stream);
+      };
+      hipError_t e = f.cu_seqlens_q ? launch_all(std::true_type{}) : launch_all(std::false_type{});
       if (e != hipSuccess) return e;
       // Varlen: a sequence longer than max_seqlen / total promised has no
       // room in the scratch; dQ from dS left its heads alone and they get
-      // the recomputed dQ here (one workgroup per sequence and head, which
-      // returns at once when its region fit).  Dense scratch is sized
-      // exactly, so no such head exists.
+      // the recomputed dQ here (one workgroup per sequence, which returns at
+      // once when its last head's region fit, and so all of them).  Dense
+      // scratch is sized exactly, so no such head exists.
       if (f.cu_seqlens_q) {
         using CQ = Dq16Cfg<D>;
         auto kq = dq16_kernel<Tag, D, MODE>;
         e = allow_lds((const void*)kq, CQ::LDS_BYTES);
         if (e != hipSuccess) return e;
         const int nq = (f.seqlen_q + CQ::BM - 1) / CQ::BM;
-        const long gq = (long)f.batch * f.heads_q;
-        hipLaunchKernelGGL(kq, dim3((unsigned)gq), dim3(CQ::NT), CQ::LDS_BYTES, stream, p, nq, 2);
+        hipLaunchKernelGGL(kq, dim3((unsigned)f.batch), dim3(CQ::NT), CQ::LDS_BYTES, stream, p, nq, 2);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
       }

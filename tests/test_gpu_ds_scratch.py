@@ -167,3 +167,41 @@ def test_phase_api_dq_needs_its_dkdv_phase_first():
     ref = _backward(do, q, k, v, out, lse, True, scale, (-1, -1), 0.0, None, None, 0.0, 0)
     torch.cuda.synchronize()
     assert torch.equal(dq, ref[0]) and torch.equal(dk, ref[1]) and torch.equal(dv, ref[2])
+
+
+@pytest.mark.parametrize("understate", [False, True])
+def test_varlen_large_batch_ds_path(understate):
+    """A batch of 150 short sequences: the dS regions of sequences past the
+    first 64 are found by more than one pass of the wave sum.  Against the
+    recompute path; with `understate`, sequence 140 is longer than
+    max_seqlen promised, so its heads (and every later sequence's, whose
+    regions start after it) fall back to the recomputed dQ."""
+    dtype = torch.float16
+    g = torch.Generator().manual_seed(21)
+    lengths = torch.randint(1, 97, (150,), generator=g).tolist()
+    mx = max(lengths)
+    if understate:
+        lengths[140] = 3 * mx
+    total = sum(lengths)
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32, device=DEVICE)
+    q, do = _rand((total, 4, 128), dtype), _rand((total, 4, 128), dtype)
+    k, v = _rand((total, 2, 128), dtype), _rand((total, 2, 128), dtype)
+
+    def fn(a, b, c):
+        return flash_attention_varlen(a, b, c, cu, cu, mx, mx, causal=True)
+
+    out_a, g_a, out_b, g_b = _both(fn, q, k, v, do)
+    if not understate:
+        assert torch.equal(out_a, out_b)
+        _check(g_a, g_b, dtype)
+        return
+    # Rows past max_seqlen of the long sequence are undefined in both paths.
+    keep = torch.ones(total, dtype=torch.bool, device=DEVICE)
+    s140 = sum(lengths[:140])
+    keep[s140 + mx: s140 + lengths[140]] = False
+    ulp = 2.0 ** -10
+    for x, y in zip(g_a[:1], g_b[:1]):
+        x, y = x[keep].float(), y[keep].float()
+        scale = y.abs().max().item()
+        assert torch.isfinite(x).all()
+        assert (x - y).abs().max().item() <= 4 * ulp * max(scale, 1e-3)
