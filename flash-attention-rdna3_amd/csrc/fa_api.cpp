@@ -160,6 +160,14 @@ size_t fa_bwd_workspace_bytes(const fa_bwd_params* params) {
   return fa::bwd_ds_bytes(*params);
 }
 
+size_t fa_bwd_workspace_min_bytes(const fa_bwd_params* params) {
+  if (!params) return 0;
+  const size_t full = fa::bwd_ds_bytes(*params);
+  const int per = (params->fwd.heads_kv + 1) / 2;
+  const size_t half = params->fwd.heads_kv > 1 ? fa::bwd_ds_chunk_bytes(*params, per) : 0;
+  return (half > 0 && fa::bwd_ds_chunk_heads(*params, (int64_t)half) == per) ? half : full;
+}
+
 // With dS scratch, phase 2 alone reads the dS that phase 1 stored there.
 // Each phase-1 launch on a scratch records what it computed (the forward
 // problem, dO, delta and the scratch size); phase 2 alone on that scratch

@@ -637,6 +637,53 @@ static hipError_t run_bwd(const fa_bwd_params& p, int phases, hipStream_t stream
     const size_t need = bwd_ds_bytes(p);
     use_ds = fast_ok && p.ds_workspace != nullptr && need > 0 && p.ds_workspace_bytes >= (int64_t)need;
   }
+  // Scratch too small for every head at once: dK/dV and dQ run in two
+  // chunks of KV heads (with their query heads), each reusing the scratch,
+  // after one delta pass over all heads, when bwd_ds_chunk_heads allows it.
+  // Only whole backwards (both passes in one call) are chunked, and only
+  // without the per-head modifiers (MODE 0: causal / window; MODE 3:
+  // softcap), whose head index would otherwise shift.
+  if constexpr (FAST && D >= 64 && (MODE == 0 || MODE == 3)) {
+    if (fast_ok && !use_ds && p.ds_workspace != nullptr && (phases & 6) == 6) {
+      const int per = bwd_ds_chunk_heads(p, p.ds_workspace_bytes);
+      if (per > 0) {
+        if (phases & 1) {
+          constexpr int rows = 16 * delta_rows_per_thread<Tag, D>();
+          const int nrb = (f.seqlen_q + rows - 1) / rows;
+          const int heads_fast = (f.out_stride[1] < f.out_stride[2] && p.dout_stride[1] < p.dout_stride[2] &&
+                                  nrb <= 65535 && f.batch <= 65535) ? 1 : 0;
+          const dim3 grid = heads_fast ? dim3(f.heads_q, nrb, f.batch) : dim3(nrb, f.batch * f.heads_q);
+          hipLaunchKernelGGL((bwd_delta_kernel<Tag, D>), grid, dim3(256), 0, stream, p, heads_fast);
+          hipError_t e = hipGetLastError();
+          if (e != hipSuccess) return e;
+        }
+        const int group = f.heads_q / f.heads_kv;
+        for (int kv0 = 0; kv0 < f.heads_kv; kv0 += per) {
+          const int n = std::min(per, f.heads_kv - kv0);
+          const int64_t h0 = (int64_t)kv0 * group;
+          fa_bwd_params c = p;
+          auto shift = [](const void* ptr, int64_t elems) {
+            return static_cast<const void*>(static_cast<const uint16_t*>(ptr) + elems);
+          };
+          c.fwd.q = shift(f.q, h0 * f.q_stride[1]);
+          c.fwd.k = shift(f.k, kv0 * f.k_stride[1]);
+          c.fwd.v = shift(f.v, kv0 * f.v_stride[1]);
+          c.fwd.out = const_cast<void*>(shift(f.out, h0 * f.out_stride[1]));
+          c.fwd.lse = f.lse + h0 * f.lse_stride[1];
+          c.dout = shift(p.dout, h0 * p.dout_stride[1]);
+          c.delta = p.delta + h0 * p.delta_stride[1];
+          c.dq = const_cast<void*>(shift(p.dq, h0 * p.dq_stride[1]));
+          c.dk = const_cast<void*>(shift(p.dk, kv0 * p.dk_stride[1]));
+          c.dv = const_cast<void*>(shift(p.dv, kv0 * p.dv_stride[1]));
+          c.fwd.heads_kv = n;
+          c.fwd.heads_q = n * group;
+          hipError_t e = run_bwd<Tag, D, MODE>(c, 6, stream);
+          if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+      }
+    }
+  }
   const bool fused_delta = fast_ok && !use_ds && (phases & 1) && (phases & 4);
   if ((phases & 1) && !fused_delta) {
     constexpr int rows = 16 * delta_rows_per_thread<Tag, D>();

@@ -47,6 +47,17 @@ __host__ __device__ inline int64_t ds_region_elems(int sq, int sk) {
   return ((int64_t)sk + kDsTileKeys - 1) / kDsTileKeys * ds_qblocks(sq) * kDsTileElems;
 }
 size_t bwd_ds_bytes(const fa_bwd_params& p);
+// dS scratch for `kv_heads` KV heads (with their query heads) of p, or 0
+// when the backward cannot run in KV-head chunks: the per-head modifiers
+// (bias, ALiBi, dropout) are indexed by the head, so only problems without
+// them are chunked.
+size_t bwd_ds_chunk_bytes(const fa_bwd_params& p, int kv_heads);
+// KV heads per chunk when a backward with `ws` bytes of dS scratch runs in
+// chunks, or 0 when it does not (the whole dS fits, or the problem cannot
+// be chunked, or chunking would not pay: it is used only for two chunks of
+// at least 1 GiB of dS each).
+int bwd_ds_chunk_heads(const fa_bwd_params& p, int64_t ws);
+constexpr int64_t kDsMinChunkBytes = int64_t(1) << 30;
 
 // Raise a kernel's dynamic LDS limit once per process (gfx950: 160 KiB/CU).
 hipError_t allow_lds(const void* kernel, int bytes);

@@ -45,9 +45,21 @@ using OptTensor = std::optional<Tensor>;
 // (zeros add nothing to q.k^T or p.v; the scale is the caller's).
 constexpr int64_t kMinKernelHeadDim = 32;
 
-// Largest dS scratch a backward allocates; above it dQ recomputes the
-// scores.  0 disables the dS path.
-std::atomic<int64_t> g_ds_limit{int64_t(8) << 30};
+// Largest dS scratch a backward allocates.  A problem whose dS exceeds it
+// runs in two chunks of KV heads when one chunk fits and the library chunks
+// it (fa_bwd_workspace_min_bytes); otherwise dQ recomputes the scores.  0
+// disables the dS path.
+std::atomic<int64_t> g_ds_limit{int64_t(12) << 30};
+
+// Scratch bytes for the backward of p under `limit`: the whole dS, else one
+// chunk's, else 0.
+int64_t ds_scratch_bytes(const fa_bwd_params& p, int64_t limit) {
+  const int64_t full = (int64_t)fa_bwd_workspace_bytes(&p);
+  if (full <= 0) return 0;
+  if (full <= limit) return full;
+  const int64_t half = (int64_t)fa_bwd_workspace_min_bytes(&p);
+  return (half > 0 && half < full && half <= limit) ? half : 0;
+}
 
 struct Options {
   bool causal;
@@ -218,11 +230,11 @@ std::tuple<Tensor, Tensor, Tensor> backward_impl(const Tensor& dout, const Tenso
   abi_strides4(p.dv_stride, dv);
   abi_strides3(p.delta_stride, delta);
   Tensor ds;
-  const int64_t need = (int64_t)fa_bwd_workspace_bytes(&p);
-  if (need > 0 && need <= g_ds_limit.load(std::memory_order_relaxed)) {
-    ds = at::empty({need}, query.options().dtype(at::kByte));
+  const int64_t bytes = ds_scratch_bytes(p, g_ds_limit.load(std::memory_order_relaxed));
+  if (bytes > 0) {
+    ds = at::empty({bytes}, query.options().dtype(at::kByte));
     p.ds_workspace = ds.data_ptr();
-    p.ds_workspace_bytes = need;
+    p.ds_workspace_bytes = bytes;
   }
   check_status(fa_bwd(&p, stream_of(query)), "fa_bwd");
   if (kdim != head_dim) {

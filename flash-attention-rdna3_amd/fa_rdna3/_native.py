@@ -125,7 +125,7 @@ _STRUCTS = (FwdParams, BwdParams, DecodeParams, PagedParams, TinyParams, AppendP
 EXPORTS = (
     "fa_abi_version", "fa_last_error_string", "fa_params_size", "fa_decode_workspace_bytes",
     "fa_decode_ticket_count",
-    "fa_fwd", "fa_bwd", "fa_bwd_phase", "fa_bwd_workspace_bytes", "fa_decode_splitk", "fa_decode_splitk_noalloc", "fa_decode_paged",
+    "fa_fwd", "fa_bwd", "fa_bwd_phase", "fa_bwd_workspace_bytes", "fa_bwd_workspace_min_bytes", "fa_decode_splitk", "fa_decode_splitk_noalloc", "fa_decode_paged",
     "fa_tiny_fwd_f32",
     "fa_kvcache_append",
     "fa_hbm_read_probe_count", "fa_hbm_read_probe_name", "fa_hbm_read_probe",
@@ -161,6 +161,8 @@ def lib():
         handle.fa_decode_workspace_bytes.argtypes = [ctypes.c_int] * 5
         handle.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
         handle.fa_bwd_workspace_bytes.argtypes = [ctypes.c_void_p]
+        handle.fa_bwd_workspace_min_bytes.restype = ctypes.c_size_t
+        handle.fa_bwd_workspace_min_bytes.argtypes = [ctypes.c_void_p]
         handle.fa_decode_ticket_count.restype = ctypes.c_size_t
         handle.fa_decode_ticket_count.argtypes = [ctypes.c_int] * 3
         for name, struct in (("fa_fwd", FwdParams), ("fa_bwd", BwdParams),
@@ -227,8 +229,10 @@ def call_bwd_phase(params, phase, device_tensor):
 
 def ds_scratch_limit():
     """Largest score-gradient (dS) scratch a backward allocates, in bytes
-    (8 GiB by default); above it dQ recomputes the scores instead of
-    reading the stored dS.  0 means the dS path is off."""
+    (12 GiB by default).  A backward whose dS exceeds it runs in two chunks
+    of KV heads when one chunk fits and the library chunks that problem
+    (fa_bwd_workspace_min_bytes); otherwise dQ recomputes the scores instead
+    of reading the stored dS.  0 means the dS path is off."""
     return int(ops().ds_scratch_limit())
 
 
@@ -238,12 +242,26 @@ def set_ds_scratch_limit(nbytes):
     return int(ops().set_ds_scratch_limit(int(nbytes)))
 
 
+def ds_scratch_bytes(full, half, limit):
+    """Scratch bytes a backward takes under `limit`: the whole dS (`full`,
+    fa_bwd_workspace_bytes), else one of the two KV-head chunks the library
+    would run (`half`, fa_bwd_workspace_min_bytes, when smaller than
+    `full`), else 0 (dQ then recomputes).  The C++ host path's rule."""
+    if full <= 0:
+        return 0
+    if full <= limit:
+        return full
+    return half if 0 < half < full and half <= limit else 0
+
+
 def attach_ds_scratch(params, device_tensor):
     """Give a filled BwdParams the dS scratch its backward can use (dQ as
     the single product dS K).  Returns the scratch tensor, which must stay
     alive until the launch is done, or None when the path does not apply."""
-    need = int(lib().fa_bwd_workspace_bytes(ctypes.byref(params)))
-    if need == 0 or need > ds_scratch_limit():
+    full = int(lib().fa_bwd_workspace_bytes(ctypes.byref(params)))
+    half = int(lib().fa_bwd_workspace_min_bytes(ctypes.byref(params)))
+    need = ds_scratch_bytes(full, half, ds_scratch_limit())
+    if need == 0:
         params.ds_workspace, params.ds_workspace_bytes = None, 0
         return None
     buf = torch.empty(need, dtype=torch.uint8, device=device_tensor.device)

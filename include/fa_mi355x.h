@@ -125,8 +125,10 @@ typedef struct fa_bwd_params {
    * dQ kernel recomputes the scores).  When non-NULL and at least
    * fa_bwd_workspace_bytes(params) bytes, the dK/dV pass stores the 16-bit
    * dS it already forms and dQ becomes the single product dS K, instead of
-   * recomputing S and dP (two of its three matrix products).  NULL, or a
-   * configuration fa_bwd_workspace_bytes returns 0 for: dQ recomputes.
+   * recomputing S and dP (two of its three matrix products).  A smaller
+   * scratch of at least fa_bwd_workspace_min_bytes(params) makes fa_bwd run
+   * dK/dV and dQ in two chunks of KV heads (large problems without bias,
+   * ALiBi or dropout).  NULL, or less than that: dQ recomputes.
    * Results agree either way to the rounding of the accumulation order. */
   void* ds_workspace;
   int64_t ds_workspace_bytes;
@@ -328,6 +330,16 @@ int fa_bwd_phase(const fa_bwd_params* params, int phase, void* stream);
  * 1 KiB; varlen, an upper bound from max_seqlen_k, total_q and batch.  With dS scratch, phase 2 of
  * fa_bwd_phase reads the dS that phase 1 stored. */
 size_t fa_bwd_workspace_bytes(const fa_bwd_params* params);
+/* No counterpart in the reference.  The smallest ds_workspace fa_bwd uses
+ * the dS path with: for a problem it chunks, the dS of ceil(heads_kv / 2)
+ * KV heads and their query heads (plus the 1 KiB slack), and fa_bwd then
+ * runs dK/dV and dQ once per half of the KV heads.  It chunks only when
+ * each half holds at least 1 GiB of dS and the problem has no bias, ALiBi
+ * or dropout (their head index would shift); smaller or more chunks measured
+ * slower than recomputing dQ.  Otherwise equal to fa_bwd_workspace_bytes
+ * (0 when the dS path does not apply).  fa_bwd_phase uses the dS path only
+ * with the full fa_bwd_workspace_bytes. */
+size_t fa_bwd_workspace_min_bytes(const fa_bwd_params* params);
 /* uint32 counters `tickets` needs: batch * heads_q * seqlen_q. */
 size_t fa_decode_ticket_count(int batch, int heads_q, int seqlen_q);
 

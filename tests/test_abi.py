@@ -102,6 +102,45 @@ def test_bwd_ds_workspace_size():
     assert lib.fa_bwd_workspace_bytes(None) == 0
 
 
+def test_bwd_ds_workspace_min_size_and_chunk_rule():
+    """fa_bwd_workspace_min_bytes: half the KV heads' share of the dS scratch
+    (the bound is linear in the heads) plus the slack, when each half holds
+    at least 1 GiB and the problem has no bias / ALiBi / dropout; the full
+    size otherwise; 0 where the dS path does not apply.  ds_scratch_bytes
+    picks the whole scratch, else one chunk's, else nothing."""
+    lib = _native.lib()
+    p = _native.BwdParams()
+    p.fwd.abi_version, p.fwd.dtype = _native.ABI_VERSION, 0
+    p.fwd.batch, p.fwd.heads_q, p.fwd.heads_kv = 1, 32, 32
+    p.fwd.seqlen_q = p.fwd.seqlen_k = 16384
+    p.fwd.head_dim = 128
+    full = lib.fa_bwd_workspace_bytes(ctypes.byref(p))
+    head = 256 * 128 * 16384  # 64-key x 128-query tiles of 16 KiB per head
+    assert full == 32 * head + 1024
+    half = lib.fa_bwd_workspace_min_bytes(ctypes.byref(p))
+    assert half == 16 * head + 1024
+    assert _native.ds_scratch_bytes(full, half, full) == full
+    assert _native.ds_scratch_bytes(full, half, full - 1) == half
+    assert _native.ds_scratch_bytes(full, half, half - 1) == 0
+    p.fwd.heads_kv = 3  # odd KV head count: ceil(3 / 2) = 2 of 3 per chunk
+    p.fwd.heads_q = 3
+    assert lib.fa_bwd_workspace_min_bytes(ctypes.byref(p)) == 2 * head + 1024
+    p.fwd.heads_q = p.fwd.heads_kv = 32
+    p.fwd.dropout_p = 0.1
+    assert lib.fa_bwd_workspace_min_bytes(ctypes.byref(p)) == full
+    p.fwd.dropout_p = 0.0
+    slopes = (ctypes.c_float * 32)()
+    p.fwd.alibi_slopes = ctypes.addressof(slopes)
+    assert lib.fa_bwd_workspace_min_bytes(ctypes.byref(p)) == full
+    p.fwd.alibi_slopes = None
+    # A half below 1 GiB of dS is not chunked: config 2 (268 MB in all).
+    p.fwd.batch, p.fwd.heads_q, p.fwd.heads_kv, p.fwd.seqlen_q, p.fwd.seqlen_k = 2, 16, 16, 2048, 2048
+    assert lib.fa_bwd_workspace_min_bytes(ctypes.byref(p)) == lib.fa_bwd_workspace_bytes(ctypes.byref(p))
+    p.fwd.head_dim = 32
+    assert lib.fa_bwd_workspace_min_bytes(ctypes.byref(p)) == 0
+    assert lib.fa_bwd_workspace_min_bytes(None) == 0
+
+
 def test_torch_host_library_registers_its_operators():
     """libfa_torch.so (the C++ host path of the dense forward / backward)
     loads with the C-ABI library and registers its operators; the dS

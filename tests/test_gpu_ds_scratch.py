@@ -7,6 +7,8 @@ both must agree to a few units of the output dtype's rounding.  Covers dense, GQ
 stored quartered), ALiBi, bias, dropout, cross shapes, head_dim 64 and varlen
 packing."""
 
+import ctypes
+
 import pytest
 import torch
 
@@ -205,3 +207,70 @@ def test_varlen_large_batch_ds_path(understate):
         scale = y.abs().max().item()
         assert torch.isfinite(x).all()
         assert (x - y).abs().max().item() <= 4 * ulp * max(scale, 1e-3)
+
+
+def _grads_at_limit(fn, tensors, limit):
+    saved = _native.set_ds_scratch_limit(limit)
+    try:
+        leaves = [t.detach().clone().requires_grad_(True) for t in tensors[:3]]
+        out = fn(*leaves)
+        out.backward(tensors[3])
+        torch.cuda.synchronize()
+        return [t.grad for t in leaves]
+    finally:
+        _native.set_ds_scratch_limit(saved)
+
+
+def _min_and_full(q, k, varlen):
+    """(one KV head's scratch, whole scratch) for these shapes, from the ABI."""
+    p = _native.BwdParams()
+    p.fwd.abi_version, p.fwd.dtype = _native.ABI_VERSION, _native.DTYPE_CODE[q.dtype]
+    p.fwd.head_dim = q.shape[-1]
+    if varlen:
+        lengths, mx = varlen
+        p.fwd.batch, p.fwd.heads_q, p.fwd.heads_kv = len(lengths), q.shape[1], k.shape[1]
+        p.fwd.seqlen_q = p.fwd.seqlen_k = mx
+        p.fwd.total_q = p.fwd.total_k = q.shape[0]
+        cu = torch.zeros(len(lengths) + 1, dtype=torch.int32)
+        p.fwd.cu_seqlens_q = p.fwd.cu_seqlens_k = cu.data_ptr()
+    else:
+        p.fwd.batch, p.fwd.heads_q, p.fwd.seqlen_q, _ = q.shape
+        p.fwd.heads_kv, p.fwd.seqlen_k = k.shape[1], k.shape[2]
+    lib = _native.lib()
+    return int(lib.fa_bwd_workspace_min_bytes(ctypes.byref(p))), int(lib.fa_bwd_workspace_bytes(ctypes.byref(p)))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("opts", [dict(causal=True), dict(causal=True, window_size=(1500, -1), softcap=30.0)])
+@pytest.mark.parametrize("varlen", [False, True])
+def test_chunked_ds_path_equals_whole_scratch(dtype, opts, varlen):
+    """A scratch of fa_bwd_workspace_min_bytes (half the KV heads' dS, at
+    least 1 GiB): dK/dV and dQ run in two chunks of KV heads, the same
+    kernels on the same heads, so every gradient is bit-identical to the
+    whole-scratch run; both agree with the recompute path."""
+    torch.manual_seed(7)
+    if varlen:
+        lengths = [8192, 5000, 3000, 7000]
+        total, mx = sum(lengths), max(lengths)
+        cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32, device=DEVICE)
+        q, do = _rand((total, 8, 128), dtype), _rand((total, 8, 128), dtype)
+        k, v = _rand((total, 4, 128), dtype), _rand((total, 4, 128), dtype)
+
+        def fn(a, b, c):
+            return flash_attention_varlen(a, b, c, cu, cu, mx, mx, **opts)
+        half, full = _min_and_full(q, k, (lengths, mx))
+    else:
+        q, do = _rand((2, 8, 8192, 128), dtype), _rand((2, 8, 8192, 128), dtype)
+        k, v = _rand((2, 4, 8192, 128), dtype), _rand((2, 4, 8192, 128), dtype)
+
+        def fn(a, b, c):
+            return flash_attention(a, b, c, **opts)
+        half, full = _min_and_full(q, k, None)
+    assert (1 << 30) < half < full
+    whole = _grads_at_limit(fn, (q, k, v, do), full)
+    chunked = _grads_at_limit(fn, (q, k, v, do), half)
+    recompute = _grads_at_limit(fn, (q, k, v, do), 0)
+    print(f"chunked dS: {half} of {full} bytes", flush=True)
+    for a, b in zip(whole, chunked):
+        assert torch.equal(a, b)
+    _check(whole, recompute, dtype)
