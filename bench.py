@@ -740,18 +740,37 @@ def pmc_summary(dirs):
 
 def stats_summary(d):
     """Markdown table of a rocprofv3 --kernel-trace --stats run
-    (--output-format csv): calls, average and total time per kernel."""
+    (--output-format csv): calls, average and total time per kernel.  With
+    the run's kernel_trace.csv present, one row per (kernel, grid size), so
+    launches of one kernel on different workloads are averaged apart."""
     import csv
     import glob
 
+    def short(name):
+        return name if len(name) <= 100 else name[:100] + "…"
+
+    traces = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+    if traces:
+        groups = {}
+        for r in csv.DictReader(open(traces[0])):
+            grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            ns = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            g = groups.setdefault((r["Kernel_Name"], grid), [0, 0])
+            g[0] += 1
+            g[1] += ns
+        total = sum(v[1] for v in groups.values()) or 1
+        print("| kernel | grid (threads) | calls | avg us | total us | % |")
+        print("|---|---|---|---|---|---|")
+        for (name, grid), (n, ns) in sorted(groups.items(), key=lambda kv: -kv[1][1]):
+            print(f"| `{short(name)}` | {grid} | {n} | {ns / n / 1e3:.2f} | {ns / 1e3:.1f} | {100.0 * ns / total:.1f} |")
+        return
     f = glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)[0]
     rows = list(csv.DictReader(open(f)))
     print("| kernel | calls | avg us | total us | % |")
     print("|---|---|---|---|---|")
     for r in rows:
-        name = r["Name"] if len(r["Name"]) <= 100 else r["Name"][:100] + "…"
-        print(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['TotalDurationNs']) / 1e3:.1f} "
-              f"| {float(r['Percentage']):.1f} |")
+        print(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+              f"{float(r['TotalDurationNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
 
 
 def traffic_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, copy_mib=256):
