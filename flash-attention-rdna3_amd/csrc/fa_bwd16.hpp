@@ -877,8 +877,12 @@ __device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blo
   // dQ sums the same products in the same order whichever step size runs,
   // so a sequence's dQ does not depend on the launch it is part of.
   constexpr int SPLIT = 32, SPS = SPLIT / C::BN;  // steps per split unit
-  lo = lo / SPLIT * SPLIT;
-  const int nsplit = (hi > lo && region >= 0) ? (hi - lo + SPLIT - 1) / SPLIT : 0;
+  // The step bounds are the same for every lane but derive from per-lane
+  // loads (cu_seqlens): kept in scalar registers so the step loop's control
+  // and waits stay scalar instead of exec-mask branches.
+  lo = __builtin_amdgcn_readfirstlane(lo / SPLIT * SPLIT);
+  hi = __builtin_amdgcn_readfirstlane(hi);
+  const int nsplit = __builtin_amdgcn_readfirstlane((hi > lo && region >= 0) ? (hi - lo + SPLIT - 1) / SPLIT : 0);
 
   const int m0w = m0 + 32 * wave;
   const int mrows = min(32, sq - m0w);
@@ -898,7 +902,8 @@ __device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blo
   const int nh0 = half0 * SPS;
   const int my_first = khalf == 0 ? 0 : nh0;
   const int my_end = min(lo + SPLIT * (khalf == 0 ? half0 : nsplit), hi);
-  const int my_count = max(0, (my_end - (lo + my_first * C::BN) + C::BN - 1) / C::BN);
+  const int my_count =
+      __builtin_amdgcn_readfirstlane(max(0, (my_end - (lo + my_first * C::BN) + C::BN - 1) / C::BN));
   S* const hsmem = smem + khalf * C::HALF;
   const uint32_t lds0 = lds_addr(hsmem);
   // Stage st holds step t with t % NSTG == st; NSTG - 1 steps are in flight
@@ -937,7 +942,7 @@ __device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blo
     __syncthreads();
     // The stage refilled here was last read in step t - 1, before the barrier.
     if (t + C::NSTG - 1 < my_count) load_stage(n0 + (C::NSTG - 1) * C::BN, (t + C::NSTG - 1) % C::NSTG);
-    const int vis = t < my_count ? bounds_vis(qvb, n0, n0 + C::BN - 1) : 0;
+    const int vis = __builtin_amdgcn_readfirstlane(t < my_count ? bounds_vis(qvb, n0, n0 + C::BN - 1) : 0);
     if (vis) {
       const S* Ks = hsmem + st * C::STAGE;
       const S* Ss = Ks + C::KT;
@@ -958,6 +963,7 @@ __device__ __forceinline__ void dqs16_item(const fa_bwd_params& p, int num_m_blo
       for (int j = 0; j < C::NPV; ++j)
 #pragma unroll
         for (int db = 0; db < C::NDB; ++db) dq[db] = EL::mma(tr_op_rowmap<D>(Ks, 0, 32 * db, j, lane), sb[j], dq[db]);
+      sched_read_ahead<C::NPV * C::NDB, 4, 2>();
     }
   }
   __syncthreads();
