@@ -274,3 +274,22 @@ def test_chunked_ds_path_equals_whole_scratch(dtype, opts, varlen):
     for a, b in zip(whole, chunked):
         assert torch.equal(a, b)
     _check(whole, recompute, dtype)
+
+
+def test_chunked_ds_path_odd_kv_heads():
+    """Three KV heads (GQA group 2) split into chunks of 2 and 1 KV heads:
+    bit-identical to the whole scratch."""
+    torch.manual_seed(8)
+    dtype = torch.float16
+    q, do = _rand((2, 6, 8192, 128), dtype), _rand((2, 6, 8192, 128), dtype)
+    k, v = _rand((2, 3, 8192, 128), dtype), _rand((2, 3, 8192, 128), dtype)
+
+    def fn(a, b, c):
+        return flash_attention(a, b, c, causal=True)
+
+    half, full = _min_and_full(q, k, None)
+    assert (half - 1024) * 3 == (full - 1024) * 2
+    whole = _grads_at_limit(fn, (q, k, v, do), full)
+    chunked = _grads_at_limit(fn, (q, k, v, do), half)
+    for a, b in zip(whole, chunked):
+        assert torch.equal(a, b)
