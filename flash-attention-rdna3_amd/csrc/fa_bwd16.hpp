@@ -294,7 +294,10 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
           sacc = EL::mma(swz_op<D>(Qs, l32, 2 * s + h), swz_op<D>(klds, l32, 2 * s + h), sacc);
           pacc = EL::mma(swz_op<D>(Gs, l32, 2 * s + h), swz_op<D>(vlds, l32, 2 * s + h), pacc);
         }
-        if constexpr (MODE == 0) sched_read_ahead<2 * C::NSTEP, 4, 2, 8>();
+        // The LDS operand reads of the score MFMAs go two MFMAs ahead (the
+        // four-ahead schedule spilled VGPRs: measured config 5's MODE 3
+        // dK/dV 766 -> 718 us, config 2's MODE 0 88.4 -> 87.9 us).
+        if constexpr (MODE == 0 || MODE == 3) sched_read_ahead<2 * C::NSTEP, 2, 2, 8>();
         // The fully visible case (no modifiers) is its own straight-line
         // body: a per-element choice would become one branch per score.
         // MASK: the block is partly visible (vis == 1); fully visible blocks
