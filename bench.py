@@ -38,7 +38,7 @@ PEAK_HBM_GBS = 8000.0
 # rocprofv3 FETCH_SIZE / WRITE_SIZE runs scaled by a 256 MiB copy
 # (profiles/cfg2_hbm_traffic.md).  The bench cannot read counters itself;
 # re-measure when the kernel changes.
-DKDV_TRAFFIC_BYTES = 323.3e6
+DKDV_TRAFFIC_BYTES = 326.9e6
 
 CFG2 = dict(batch=2, heads=16, seqlen=2048, head_dim=128, causal=True, dtype=torch.float16)
 
