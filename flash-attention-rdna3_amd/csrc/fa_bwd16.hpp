@@ -371,7 +371,8 @@ __global__ __launch_bounds__(512, 1) void dkdv16_kernel(fa_bwd_params p, int num
             dv[db] = EL::mma(tr_op_rowmap<D>(Gs, 0, 32 * db, j, lane), pb[j], dv[db]);
             dk[db] = EL::mma(tr_op_rowmap<D>(Qs, 0, 32 * db, j, lane), sb[j], dk[db]);
           }
-        if constexpr (MODE == 0) sched_read_ahead<2 * C::NPV * C::NDB, 4, 2>();
+        // Two ahead here too (config 2's dK/dV 90.3 -> 89.1 us against four).
+        if constexpr (MODE == 0) sched_read_ahead<2 * C::NPV * C::NDB, 2, 2>();
         if (t + 1 < my_count) store_stage(st ^ 1, m0 + C::BMQ);
         if (ds_on) {
           // Operand j of lane half h holds rows 16j + 4h + e and
